@@ -1,0 +1,334 @@
+"""Python binding of the MI355X inference backend's C ABI (include/azgo_hip.h).
+
+A thin ctypes layer used by the tests and the benchmark; the product is
+libazgo_hip.so, which it loads from this directory. There is no fallback: if
+the library is missing, loading raises, and every call that needs the GPU
+fails with the library's own error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libazgo_hip.so")
+
+OK = 0
+ERR_ARGUMENT, ERR_UNAVAILABLE, ERR_MEMORY, ERR_TENSOR, ERR_HIP, ERR_STATE = -1, -2, -3, -4, -5, -6
+
+
+class NetCfg(C.Structure):
+    """azh_netcfg (NetConfig, include/azgo/network.hpp:24-36)."""
+    _fields_ = [("board", C.c_int), ("history", C.c_int), ("blocks", C.c_int),
+                ("filters", C.c_int), ("value_hidden", C.c_int), ("ownership", C.c_int)]
+
+    @property
+    def planes(self):
+        return 2 * self.history + 2
+
+    @property
+    def area(self):
+        return self.board * self.board
+
+    @property
+    def actions(self):
+        return self.area + 1
+
+
+class Tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", C.POINTER(C.c_float)), ("size", C.c_size_t)]
+
+
+DONE_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_char_p)
+
+
+class HipError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+
+
+def load():
+    """The native library, loaded once. Raises if it is not built."""
+    if not hasattr(load, "lib"):
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"azgo_hip: native library missing: {LIB_PATH} (build it with "
+                               f"alphazero-go_amd/build.py)")
+        h = C.CDLL(LIB_PATH)
+        P = C.POINTER
+        f32, u8, vp = P(C.c_float), P(C.c_uint8), C.c_void_p
+        sig = {
+            "azh_built": ([], C.c_int),
+            "azh_available": ([C.c_char_p, C.c_size_t], C.c_int),
+            "azh_describe": ([C.c_char_p, C.c_size_t], C.c_int),
+            "azh_last_error": ([], C.c_char_p),
+            "azh_memory_need": ([P(NetCfg), C.c_int, C.c_int, P(C.c_size_t)], C.c_int),
+            "azh_check_memory": ([P(NetCfg), C.c_int, C.c_int, C.c_int], C.c_int),
+            "azh_create": ([P(NetCfg), P(Tensor), C.c_int, C.c_int, C.c_int, P(vp)], C.c_int),
+            "azh_destroy": ([vp], None),
+            "azh_slots": ([vp], C.c_int),
+            "azh_max_batch": ([vp], C.c_int),
+            "azh_slot_input": ([vp, C.c_int], f32),
+            "azh_slot_logits": ([vp, C.c_int], f32),
+            "azh_slot_values": ([vp, C.c_int], f32),
+            "azh_begin": ([vp, C.c_int, C.c_int, DONE_FN, vp], C.c_int),
+            "azh_infer": ([vp, f32, C.c_int, f32, f32], C.c_int),
+            "azh_softmax_legal": ([f32, u8, C.c_int, C.c_int, f32], C.c_int),
+            "azh_set_graphs": ([vp, C.c_int], C.c_int),
+            "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
+            "azh_enqueue": ([vp, C.c_int, C.c_int], C.c_int),
+            "azh_synchronize": ([vp, C.c_int], C.c_int),
+            "azh_fetch": ([vp, C.c_int, C.c_int], C.c_int),
+            "azh_time_passes": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_time_trunk_conv": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_time_round_trips": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                   f32], C.c_int),
+            "azh_probe_heads": ([vp, f32, C.c_int, f32, f32], C.c_int),
+            "azh_probe_trunk": ([vp, f32, C.c_int, C.c_int, f32], C.c_int),
+            "azh_probe_fill": ([f32, C.c_size_t, C.c_float, C.c_size_t], C.c_int),
+            "azh_probe_copy": ([C.c_size_t, C.c_int, f32], C.c_int),
+            "azh_set_hub_chaos_seed": ([C.c_uint64], None),
+            "azh_hub_chaos_seed": ([], C.c_uint64),
+            "azh_fail_passes_after": ([C.c_int], None),
+            "azh_set_memory_limit": ([C.c_size_t], None),
+            "azh_passes_completed": ([], C.c_longlong),
+            "azh_set_copy_out_delay": ([C.c_int], None),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = res
+        load.lib = h
+        load.symbols = sorted(sig)
+    return load.lib
+
+
+def _check(rc):
+    if rc != OK:
+        raise HipError(rc, load().azh_last_error().decode())
+
+
+def _f(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def available():
+    """(usable, why)."""
+    buf = C.create_string_buffer(512)
+    ok = load().azh_available(buf, 512)
+    return bool(ok), buf.value.decode()
+
+
+def describe():
+    buf = C.create_string_buffer(512)
+    _check(load().azh_describe(buf, 512))
+    return buf.value.decode()
+
+
+def net_cfg(board, history, blocks, filters, value_hidden, ownership=0):
+    return NetCfg(board, history, blocks, filters, value_hidden, ownership)
+
+
+def memory_need(cfg, max_batch, slots):
+    n = C.c_size_t()
+    _check(load().azh_memory_need(C.byref(cfg), max_batch, slots, C.byref(n)))
+    return n.value
+
+
+def check_memory(cfg, max_batch, hubs, slots_per_hub=2):
+    _check(load().azh_check_memory(C.byref(cfg), max_batch, hubs, slots_per_hub))
+
+
+class Runner:
+    """An azh_runner: the network's weights on the GPU, `slots` slots of up to
+    max_batch positions. tensors: {name: float array} of the network's
+    params() and buffers()."""
+
+    def __init__(self, cfg: NetCfg, tensors: dict, max_batch: int, slots: int = 2):
+        self.lib = load()
+        self.cfg = cfg
+        arrays = [(k.encode(), _f32(v)) for k, v in tensors.items()]
+        table = (Tensor * len(arrays))()
+        for i, (k, v) in enumerate(arrays):
+            table[i] = Tensor(k, _f(v), v.size)
+        h = C.c_void_p()
+        _check(self.lib.azh_create(C.byref(cfg), table, len(arrays), max_batch, slots, C.byref(h)))
+        self.h = h
+        self.max_batch = max_batch
+        self._callbacks = {}
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.azh_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def slots(self):
+        return self.lib.azh_slots(self.h)
+
+    def infer(self, inp):
+        inp = _f32(inp)
+        B = inp.shape[0]
+        logits = np.empty((B, self.cfg.actions), np.float32)
+        values = np.empty(B, np.float32)
+        _check(self.lib.azh_infer(self.h, _f(inp), B, _f(logits), _f(values)))
+        return logits, values
+
+    def set_graphs(self, enabled):
+        _check(self.lib.azh_set_graphs(self.h, int(enabled)))
+
+    # ---- slot staging (the hub's view)
+    def input(self, slot):
+        p = self.lib.azh_slot_input(self.h, slot)
+        n = self.max_batch * self.cfg.planes * self.cfg.area
+        return np.ctypeslib.as_array(p, (n,)).reshape(self.max_batch, self.cfg.planes, self.cfg.area)
+
+    def logits(self, slot, B):
+        p = self.lib.azh_slot_logits(self.h, slot)
+        return np.ctypeslib.as_array(p, (self.max_batch * self.cfg.actions,)).reshape(
+            self.max_batch, self.cfg.actions)[:B].copy()
+
+    def values(self, slot, B):
+        p = self.lib.azh_slot_values(self.h, slot)
+        return np.ctypeslib.as_array(p, (self.max_batch,))[:B].copy()
+
+    def begin(self, slot, B, done):
+        """done(slot, error_or_None) from the completion thread."""
+        key = (slot, threading.get_ident(), len(self._callbacks))
+
+        def cb(user, s, err, _key=key):
+            try:
+                done(s, err.decode() if err else None)
+            finally:
+                pass
+
+        fn = DONE_FN(cb)
+        self._callbacks[key] = fn   # kept alive until the runner goes
+        _check(self.lib.azh_begin(self.h, slot, B, fn, None))
+
+    # ---- device-resident passes
+    def stage(self, slot, B):
+        _check(self.lib.azh_stage(self.h, slot, B))
+
+    def enqueue(self, slot, B):
+        _check(self.lib.azh_enqueue(self.h, slot, B))
+
+    def synchronize(self, slot):
+        _check(self.lib.azh_synchronize(self.h, slot))
+
+    def fetch(self, slot, B):
+        _check(self.lib.azh_fetch(self.h, slot, B))
+        return self.logits(slot, B), self.values(slot, B)
+
+    def time_passes(self, slot, B, iters):
+        ms = C.c_float()
+        _check(self.lib.azh_time_passes(self.h, slot, B, iters, C.byref(ms)))
+        return ms.value
+
+    def time_trunk_conv(self, slot, B, iters):
+        ms = C.c_float()
+        _check(self.lib.azh_time_trunk_conv(self.h, slot, B, iters, C.byref(ms)))
+        return ms.value
+
+    def time_round_trips(self, slot, B, iters):
+        ms = C.c_float()
+        _check(self.lib.azh_time_round_trips(self.h, slot, B, iters, C.byref(ms)))
+        return ms.value
+
+    # ---- probes
+    def probe_heads(self, trunk):
+        trunk = _f32(trunk)
+        B = trunk.shape[0]
+        logits = np.empty((B, self.cfg.actions), np.float32)
+        values = np.empty(B, np.float32)
+        _check(self.lib.azh_probe_heads(self.h, _f(trunk), B, _f(logits), _f(values)))
+        return logits, values
+
+    def probe_trunk(self, inp, blocks):
+        inp = _f32(inp)
+        B = inp.shape[0]
+        out = np.empty((B, self.cfg.filters, self.cfg.area), np.float32)
+        _check(self.lib.azh_probe_trunk(self.h, _f(inp), B, blocks, _f(out)))
+        return out
+
+
+def softmax_legal(logits, legal):
+    logits = _f32(logits)
+    legal = np.ascontiguousarray(legal, np.uint8)
+    B, A1 = logits.shape
+    out = np.empty_like(logits)
+    _check(load().azh_softmax_legal(_f(logits), legal.ctypes.data_as(C.POINTER(C.c_uint8)), B, A1, _f(out)))
+    return out
+
+
+def probe_conv3x3(x, w, scale, shift, skip=None, relu=True, tiling=-1):
+    """x [B][cin][n*n], w [cout][cin*9] -> y [B][cout][n*n]."""
+    x = _f32(x)
+    w = _f32(w)
+    B, cin, A = x.shape
+    n = int(round(A ** 0.5))
+    cout = w.shape[0]
+    y = np.empty((B, cout, A), np.float32)
+    sk = _f32(skip) if skip is not None else None
+    _check(load().azh_probe_conv3x3(_f(x), _f(w), _f(_f32(scale)), _f(_f32(shift)),
+                                    _f(sk) if sk is not None else None, int(relu), B, n, cin, cout, tiling, _f(y)))
+    return y
+
+
+def probe_fill(data, n, value, tail=0):
+    data = _f32(data).copy()
+    _check(load().azh_probe_fill(_f(data), n, value, tail))
+    return data
+
+
+def probe_copy(nbytes, iters):
+    ms = C.c_float()
+    _check(load().azh_probe_copy(nbytes, iters, C.byref(ms)))
+    return ms.value
+
+
+def set_hub_chaos_seed(seed):
+    load().azh_set_hub_chaos_seed(seed)
+
+
+def hub_chaos_seed():
+    return load().azh_hub_chaos_seed()
+
+
+def fail_passes_after(n):
+    load().azh_fail_passes_after(n)
+
+
+def set_memory_limit(nbytes):
+    load().azh_set_memory_limit(nbytes)
+
+
+def passes_completed():
+    return load().azh_passes_completed()
+
+
+def set_copy_out_delay(us):
+    load().azh_set_copy_out_delay(us)
+
+
+def exported_symbols():
+    """The C ABI's symbols this binding declares (include/azgo_hip.h)."""
+    load()
+    return list(load.symbols)

@@ -1,0 +1,380 @@
+// The gfx950 kernels of the inference pass.
+//
+// conv3x3: the stem and residual-tower convolutions as an implicit GEMM on
+// fp32 MFMA (v_mfma_f32_16x16x4_f32), no im2col buffer. A workgroup owns one
+// position (board) and a tile of output channels. For each chunk of 16
+// input channels it stages the board's planes in LDS with a one-point zero
+// halo ((n+2) x (n+2) per channel, four channels interleaved per point so a
+// lane fetches four K values with one ds_read_b128); the nine taps are then
+// constant offsets into that tile, so the inner loop is LDS reads with
+// immediate offsets and MFMAs, and the im2col matrix never exists. The
+// chunks are double-buffered: the next chunk's global loads are in flight
+// while the current one is multiplied. Weights come pre-packed in MFMA
+// fragment order straight from global memory (one coalesced dwordx4 per lane
+// per fragment quad; every workgroup reads the same 0.6 MB per layer, which
+// stays in L2). BN (scale, shift), the residual add and ReLU are applied to
+// the accumulators before the single store.
+//
+// MFMA operand layout (16x16x4 f32, wave64): A[i][k] comes from lane
+// i + 16k, B[k][j] from lane j + 16k, and lane j + 16g holds D[4g + r][j] in
+// accumulator element r.
+#include "azh_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+#include <cmath>
+
+namespace azh {
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+struct Geo {
+    static constexpr int A = N * N;            // points per plane
+    static constexpr int H = N + 2;            // haloed row length
+    static constexpr int HA = H * H;           // haloed plane (float4 units per group)
+    static constexpr int NPG = (A + 15) / 16;  // 16-point MFMA column groups
+    static constexpr int BUF = 4 * HA;         // float4 units of one LDS buffer (4 groups)
+};
+
+// y = relu?(scale * acc + shift (+ skip)), each operation rounded on its own.
+__device__ inline float epilogue(float acc, float s, float h, const float* skip, bool relu) {
+    float v = __fadd_rn(__fmul_rn(s, acc), h);
+    if (skip) v = __fadd_rn(v, *skip);
+    if (relu) v = v > 0.0f ? v : 0.0f;   // -0 and NaN become +0 (reluForward)
+    return v;
+}
+
+template <int N, int COW, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restrict__ x, const f4* __restrict__ wp,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ shift, const float* skip,
+                                                            float* y, int cin, int cout, int nq, int coTiles,
+                                                            int relu) {
+    using G = Geo<N>;
+    constexpr int THREADS = WAVES * 64;
+    constexpr int ITEMS = 4 * G::A;   // (channel group, point) pairs per chunk
+    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
+    __shared__ f4 lds[2 * G::BUF];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
+    // co tiles of one board run on the same XCD and share its L2.
+    const int total = gridDim.x;
+    const int wg = blockIdx.x;
+    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
+    const int b = logical / coTiles, ct = logical % coTiles;
+    const int coBlocks = (cout + 15) >> 4;
+    const int cb0 = (ct * WAVES + wave) * COW;
+    const int k = lane >> 4, n16 = lane & 15;
+
+    for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Each lane's LDS read position per column group (float4 units), taps
+    // and buffers added as constants. Points past the board read a valid
+    // cell; their outputs are never stored.
+    int rofs[G::NPG];
+#pragma unroll
+    for (int pg = 0; pg < G::NPG; ++pg) {
+        int p = pg * 16 + n16;
+        p = p < G::A ? p : G::A - 1;
+        rofs[pg] = k * G::HA + (p / N) * G::H + (p % N);
+    }
+
+    const float* xb = x + (size_t)b * cin * G::A;
+    f4 stage[PER];
+    auto load = [&](int q) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                const int c0 = q * 16 + 4 * g;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+            }
+            stage[r] = v;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                lds[buf * G::BUF + g * G::HA + (p / N + 1) * G::H + (p % N + 1)] = stage[r];
+            }
+        }
+    };
+
+    f4 acc[COW][G::NPG];
+#pragma unroll
+    for (int c = 0; c < COW; ++c)
+#pragma unroll
+        for (int pg = 0; pg < G::NPG; ++pg) acc[c][pg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    load(0);
+    __syncthreads();   // the zero fill is complete before any interior store
+    store(0);
+    __syncthreads();
+
+    for (int q = 0; q < nq; ++q) {
+        if (q + 1 < nq) load(q + 1);
+        const f4* buf = lds + (q & 1) * G::BUF;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            const int toff = (t / 3) * G::H + (t % 3);
+            f4 a[COW];
+#pragma unroll
+            for (int c = 0; c < COW; ++c)
+                a[c] = (cb0 + c < coBlocks) ? wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane]
+                                            : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int pg = 0; pg < G::NPG; ++pg) {
+                const f4 bv = buf[rofs[pg] + toff];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int c = 0; c < COW; ++c)
+                        acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][j], bv[j], acc[c][pg], 0, 0, 0);
+            }
+        }
+        if (q + 1 < nq) store((q + 1) & 1);
+        __syncthreads();
+    }
+
+    const float* skipb = skip ? skip + (size_t)b * cout * G::A : nullptr;
+    float* yb = y + (size_t)b * cout * G::A;
+#pragma unroll
+    for (int c = 0; c < COW; ++c) {
+        const int coBase = (cb0 + c) * 16 + 4 * k;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int co = coBase + r;
+            if (co >= cout) continue;
+            const float s = scale[co], h = shift[co];
+#pragma unroll
+            for (int pg = 0; pg < G::NPG; ++pg) {
+                const int p = pg * 16 + n16;
+                if (p < G::A) {
+                    const size_t o = (size_t)co * G::A + p;
+                    yb[o] = epilogue(acc[c][pg][r], s, h, skipb ? skipb + o : nullptr, relu != 0);
+                }
+            }
+        }
+    }
+}
+
+template <int N, int COW, int WAVES>
+hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
+                       float* y, int B, int cin, int cout, bool relu, hipStream_t stream) {
+    const int coTile = 16 * COW * WAVES;
+    const int coTiles = ceilDiv(cout, coTile);
+    const int nq = ceilDiv(cin, kChunk);
+    const dim3 grid(B * coTiles), block(WAVES * 64);
+    hipLaunchKernelGGL((conv3x3Kernel<N, COW, WAVES>), grid, block, 0, stream, x,
+                       reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
+                       relu ? 1 : 0);
+    return hipGetLastError();
+}
+
+template <int N>
+hipError_t launchConvN(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
+                       float* y, int B, int cin, int cout, bool relu, ConvTiling t, hipStream_t stream) {
+    if (t.coPerWave == 2 && t.waves == 4) return launchConvT<N, 2, 4>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    if (t.coPerWave == 2 && t.waves == 2) return launchConvT<N, 2, 2>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    if (t.coPerWave == 1 && t.waves == 4) return launchConvT<N, 1, 4>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    if (t.coPerWave == 1 && t.waves == 2) return launchConvT<N, 1, 2>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    if (t.coPerWave == 1 && t.waves == 1) return launchConvT<N, 1, 1>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------ heads
+
+template <int N>
+__global__ __launch_bounds__(256) void headsKernel(const float* __restrict__ trunk, HeadWeights w,
+                                                   float* __restrict__ logits, float* __restrict__ values, int F,
+                                                   int V) {
+    constexpr int A = N * N, A1 = A + 1;
+    __shared__ float act[3 * A];   // policy planes 0 and 1 (the flattened [2A] row), then the value plane
+    __shared__ float hid[256];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float* tb = trunk + (size_t)b * F * A;
+
+    // 1x1 convs F -> 3, BN, ReLU (src/network.cpp:274-277, 288-291).
+    for (int p = tid; p < A; p += 256) {
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
+        for (int c = 0; c < F; ++c) {
+            const float xv = tb[(size_t)c * A + p];
+            a0 = fmaf(w.convW[c], xv, a0);
+            a1 = fmaf(w.convW[F + c], xv, a1);
+            a2 = fmaf(w.convW[2 * F + c], xv, a2);
+        }
+        act[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
+        act[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
+        act[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
+    }
+    __syncthreads();
+
+    // Policy Linear: logits = flat . W^T, then + b (src/layers.cpp:169-176).
+    for (int a = tid; a < A1; a += 256) {
+        float s = 0.0f;
+        const float* wc = w.policyWT + a;
+        for (int i = 0; i < 2 * A; ++i) s = fmaf(act[i], wc[(size_t)i * A1], s);
+        logits[(size_t)b * A1 + a] = __fadd_rn(s, w.policyB[a]);
+    }
+    // Value Linear A -> V, + b, ReLU.
+    for (int v = tid; v < V; v += 256) {
+        float s = 0.0f;
+        const float* wc = w.fc1WT + v;
+        for (int p = 0; p < A; ++p) s = fmaf(act[2 * A + p], wc[(size_t)p * V], s);
+        s = __fadd_rn(s, w.fc1B[v]);
+        hid[v] = s > 0.0f ? s : 0.0f;
+    }
+    __syncthreads();
+    // Value Linear V -> 1, + b, tanh.
+    if (tid == 0) {
+        float s = 0.0f;
+        for (int v = 0; v < V; ++v) s = fmaf(hid[v], w.fc2W[v], s);
+        values[b] = tanhf(__fadd_rn(s, w.fc2B[0]));
+    }
+}
+
+// ------------------------------------------------------------------ softmax over legal moves
+
+__global__ __launch_bounds__(256) void softmaxLegalKernel(const float* __restrict__ logits,
+                                                          const uint8_t* __restrict__ legal,
+                                                          float* __restrict__ priors, int B, int actions) {
+    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (pos >= B) return;   // a whole wave leaves together
+    const float* l = logits + (size_t)pos * actions;
+    const uint8_t* m = legal + (size_t)pos * actions;
+    float* o = priors + (size_t)pos * actions;
+    float mx = -INFINITY;
+    for (int a = lane; a < actions; a += 64)
+        if (m[a] && l[a] > mx) mx = l[a];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (mx == -INFINITY) {   // no legal action: nothing to normalise
+        for (int a = lane; a < actions; a += 64) o[a] = 0.0f;
+        return;
+    }
+    float sum = 0.0f;
+    for (int a = lane; a < actions; a += 64)
+        if (m[a]) sum += expf(l[a] - mx);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    for (int a = lane; a < actions; a += 64) o[a] = m[a] ? expf(l[a] - mx) / sum : 0.0f;
+}
+
+// ------------------------------------------------------------------ test hooks
+
+__global__ void spinKernel(unsigned long long ticks) {
+    const unsigned long long start = wall_clock64();
+    unsigned long long spins = 0;
+    // Bounded twice over: by the clock, and by a spin count far above any
+    // delay a test asks for, so the wave always finishes.
+    while (wall_clock64() - start < ticks && spins < (1ull << 34)) ++spins;
+}
+
+__global__ void fillKernel(float* data, size_t n, float value) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) data[i] = value;
+}
+
+} // namespace
+
+// ------------------------------------------------------------------ host side
+
+size_t packedConv3x3Floats(int cin, int cout) {
+    return (size_t)ceilDiv(cout, kCoBlock) * ceilDiv(cin, kChunk) * 9 * 64 * 4;
+}
+
+std::vector<float> packConv3x3(const float* w, int cin, int cout) {
+    const int coBlocks = ceilDiv(cout, kCoBlock), nq = ceilDiv(cin, kChunk);
+    std::vector<float> out(packedConv3x3Floats(cin, cout), 0.0f);
+    for (int cb = 0; cb < coBlocks; ++cb)
+        for (int q = 0; q < nq; ++q)
+            for (int t = 0; t < 9; ++t)
+                for (int lane = 0; lane < 64; ++lane)
+                    for (int j = 0; j < 4; ++j) {
+                        const int co = cb * 16 + (lane & 15);
+                        const int ci = q * 16 + 4 * (lane >> 4) + j;
+                        const size_t o = ((((size_t)cb * nq + q) * 9 + t) * 64 + lane) * 4 + j;
+                        if (co < cout && ci < cin) out[o] = w[((size_t)co * cin + ci) * 9 + t];
+                    }
+    return out;
+}
+
+bool conv3x3Supported(int n) { return n == 5 || n == 9 || n == 13 || n == 19; }
+
+ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
+    (void)boardSize;
+    // Enough workgroups to cover the 256 CUs where the batch is small;
+    // otherwise the widest tile (fewest re-reads of the board in LDS).
+    const int coBlocks = ceilDiv(cout, kCoBlock);
+    if (coBlocks >= 8 && B >= 128) return {2, 4};
+    if (coBlocks >= 4 && B >= 64) return {2, 2};
+    if (coBlocks >= 4) return {1, 4};
+    if (coBlocks >= 2) return {1, 2};
+    return {1, 1};
+}
+
+hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
+                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, ConvTiling t,
+                         hipStream_t stream) {
+    if (B < 1) return hipSuccess;
+    switch (n) {
+    case 5: return launchConvN<5>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+    case 9: return launchConvN<9>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+    case 13: return launchConvN<13>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+    case 19: return launchConvN<19>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* logits, float* values, int B, int n, int F,
+                       int V, hipStream_t stream) {
+    if (B < 1) return hipSuccess;
+    if (V > 256) return hipErrorInvalidValue;
+    const dim3 grid(B), block(256);
+    switch (n) {
+    case 5: hipLaunchKernelGGL(headsKernel<5>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
+    case 9: hipLaunchKernelGGL(headsKernel<9>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
+    case 13: hipLaunchKernelGGL(headsKernel<13>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
+    case 19: hipLaunchKernelGGL(headsKernel<19>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launchSoftmaxLegal(const float* logits, const uint8_t* legal, float* priors, int B, int actions,
+                              hipStream_t stream) {
+    if (B < 1) return hipSuccess;
+    hipLaunchKernelGGL(softmaxLegalKernel, dim3(ceilDiv(B, 4)), dim3(256), 0, stream, logits, legal, priors, B,
+                       actions);
+    return hipGetLastError();
+}
+
+hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream) {
+    int khz = 0;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess) return e;
+    if (khz <= 0) khz = 100000;
+    const unsigned long long ticks = nanoseconds * (unsigned long long)khz / 1000000ull;
+    hipLaunchKernelGGL(spinKernel, dim3(1), dim3(1), 0, stream, ticks);
+    return hipGetLastError();
+}
+
+hipError_t launchFill(float* data, size_t n, float value, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fillKernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, data, n, value);
+    return hipGetLastError();
+}
+
+} // namespace azh

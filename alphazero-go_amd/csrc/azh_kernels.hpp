@@ -1,0 +1,84 @@
+// Kernel interface of the MI355X (gfx950) inference pass: launchers for the
+// fused 3x3 convolution, the fused heads and the legal-move softmax, plus
+// the host-side weight packing the convolution reads.
+//
+// Activations live in HBM board-major: [B][C][n*n] fp32, one contiguous
+// plane of n*n points per (position, channel). The network input arrives in
+// exactly that layout ([B][planes][n*n], Evaluator::evaluate's input,
+// include/azgo/evaluator.hpp:24), so the stem reads it in place.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace azh {
+
+// Channels per K chunk of the convolution: 4 groups of 4 channels.
+constexpr int kChunk = 16;
+// Output channels per MFMA block (v_mfma_f32_16x16x4_f32: 16 x 16 outputs).
+constexpr int kCoBlock = 16;
+
+inline int ceilDiv(int a, int b) { return (a + b - 1) / b; }
+
+// A 3x3 convolution's weights w [cout][cin][3][3] (Conv2d::w,
+// include/azgo/layers.hpp:32, row (c*3 + dy)*3 + dx) packed as the MFMA A
+// fragments the kernel loads: [co block][chunk q][tap t][lane 0..63][j 0..3],
+// value w[cb*16 + (lane & 15)][q*16 + 4*(lane >> 4) + j][t], zero where the
+// output or input channel is padding. coBlocks = ceil(cout/16),
+// chunks = ceil(cin/16).
+std::vector<float> packConv3x3(const float* w, int cin, int cout);
+size_t packedConv3x3Floats(int cin, int cout);
+
+// How a convolution launch is cut: output channels per workgroup (a
+// multiple of 16) and the resulting number of co tiles. The cut only
+// decides which workgroup computes an output, never how: every output
+// channel sums its inputs in one fixed order (chunk, tap, channel-in-chunk),
+// so results are bitwise independent of the cut and of the batch.
+struct ConvTiling {
+    int coPerWave;   // MFMA co blocks per wave: 1 or 2
+    int waves;       // waves per workgroup: 1, 2 or 4
+    int coTile() const { return 16 * coPerWave * waves; }
+};
+ConvTiling chooseConvTiling(int cout, int B, int boardSize);
+
+// y[b][co][p] = relu?( (scale[co] * conv(x)[b][co][p] + shift[co]) (+ skip[b][co][p]) )
+// with each multiply and add rounded separately (BatchNorm2d::forwardInfer,
+// src/layers.cpp:88-97, then the skip add and reluForward,
+// src/network.cpp:264-271). skip may alias y (in-place residual).
+// x [B][cin][n*n], y and skip [B][cout][n*n].
+hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
+                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, ConvTiling tiling,
+                         hipStream_t stream);
+bool conv3x3Supported(int boardSize);
+
+// The policy and value heads of one position per workgroup, fused:
+// 1x1 convs F -> 2 and F -> 1 with BN and ReLU, the policy Linear
+// (2A -> A+1) and the value Linears (A -> V, ReLU, V -> 1) and tanh
+// (src/network.cpp:274-296).
+struct HeadWeights {
+    const float* convW;      // [3][F]: policy rows 0-1, value row 2
+    const float* scale;      // [3] folded BN scale
+    const float* shift;      // [3] folded BN shift
+    const float* policyWT;   // [2A][A+1]: policy.fc.w transposed
+    const float* policyB;    // [A+1]
+    const float* fc1WT;      // [A][V]: value.fc1.w transposed
+    const float* fc1B;       // [V]
+    const float* fc2W;       // [V]
+    const float* fc2B;       // [1]
+};
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* logits, float* values, int B, int n, int F,
+                       int V, hipStream_t stream);
+
+// priors[b][a] = exp(l - max) / sum over legal a of the same, 0 where
+// illegal (Mcts::expand's softmax, src/mcts.cpp:170-183). One wavefront per
+// position. legal [B][actions] bytes (nonzero = legal).
+hipError_t launchSoftmaxLegal(const float* logits, const uint8_t* legal, float* priors, int B, int actions,
+                              hipStream_t stream);
+
+// Test hooks: holds the stream for about `nanoseconds` (a bounded wait on the
+// wall clock), and fills data[0..n) with value.
+hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream);
+hipError_t launchFill(float* data, size_t n, float value, hipStream_t stream);
+
+} // namespace azh

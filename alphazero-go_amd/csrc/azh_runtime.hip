@@ -1,0 +1,969 @@
+// The runtime behind include/azgo_hip.h: device context and architecture
+// check, the upload contract (named tensors, checked against the network's
+// params() and buffers()), weight packing and BN folding, per-slot device
+// workspaces with pinned staging and their own stream, the pass as one
+// hipGraph per batch size, the completion thread, timing entry points,
+// kernel probes and the test hooks.
+//
+// Compiled with -ffp-contract=off (host and device), so the host-side BN
+// fold rounds exactly as BatchNorm2d::forwardInfer does (src/layers.cpp:91-92).
+#include "azgo_hip.h"
+#include "azh_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <condition_variable>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#ifndef AZH_KERNEL_HASH
+#define AZH_KERNEL_HASH "unhashed"
+#endif
+
+namespace {
+
+thread_local std::string gLastError;
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(AZH_ERR_HIP, std::string("hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+template <class Fn>
+int guarded(Fn&& fn) {
+    try {
+        fn();
+        return AZH_OK;
+    } catch (const Error& e) {
+        gLastError = e.what();
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        gLastError = "hip: host memory exhausted";
+        return AZH_ERR_MEMORY;
+    } catch (const std::exception& e) {
+        gLastError = e.what();
+        return AZH_ERR_HIP;
+    }
+}
+
+// Test hooks (cuda_probe's, src/cuda/cuda_runner.cu:39-45).
+std::atomic<uint64_t> gHubChaosSeed{0};
+std::atomic<int> gFailCountdown{0};
+std::atomic<size_t> gMemoryLimit{0};
+std::atomic<long long> gPassesCompleted{0};
+std::atomic<int> gCopyOutDelayUs{0};
+
+// Free memory a check leaves for everything else (src/cuda/cuda_runner.cu:50).
+constexpr size_t kMemoryMargin = size_t(512) << 20;
+// The completion thread's polling interval, first and longest
+// (src/cuda/cuda_runner.cu:47): it sleeps instead of spinning a core that
+// the tree search needs.
+constexpr int kPollFirstUs = 50, kPollLastUs = 200;
+constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
+
+// ---------------------------------------------------------------- context
+
+struct Context {
+    bool ok = false;
+    std::string why, name, arch;
+    int runtime = 0;
+
+    static Context& get() {
+        static Context c;
+        return c;
+    }
+
+  private:
+    Context() {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count < 1) {
+            why = "no HIP device";
+            return;
+        }
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) {
+            why = "cannot query the HIP device";
+            return;
+        }
+        name = p.name;
+        arch = p.gcnArchName;
+        const std::string base = arch.substr(0, arch.find(':'));
+        (void)hipRuntimeGetVersion(&runtime);
+        if (base != "gfx950") {
+            why = "kernels built for gfx950; this GPU is " + base;
+            return;
+        }
+        // A first kernel, so a missing or unloadable code object shows here.
+        float* d = nullptr;
+        float h[16] = {};
+        if (hipMalloc(&d, sizeof h) != hipSuccess) {
+            why = "cannot allocate device memory";
+            return;
+        }
+        const bool ran = azh::launchFill(d, 16, 3.0f, nullptr) == hipSuccess &&
+                         hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess && h[0] == 3.0f &&
+                         h[15] == 3.0f;
+        (void)hipFree(d);
+        if (!ran) {
+            why = "the first kernel did not run";
+            return;
+        }
+        ok = true;
+    }
+};
+
+void requireContext() {
+    Context& c = Context::get();
+    if (!c.ok) throw Error(AZH_ERR_UNAVAILABLE, "hip: no usable GPU (" + c.why + ")");
+}
+
+// ---------------------------------------------------------------- network shape
+
+struct Shape {
+    int n, H, P, A, A1, F, V, blocks;
+    explicit Shape(const azh_netcfg& c)
+        : n(c.board), H(c.history), P(2 * c.history + 2), A(c.board * c.board), A1(c.board * c.board + 1),
+          F(c.filters), V(c.value_hidden), blocks(c.blocks) {}
+};
+
+void validate(const azh_netcfg* c) {
+    if (!c) throw Error(AZH_ERR_ARGUMENT, "hip: no network config");
+    if (!azh::conv3x3Supported(c->board))
+        throw Error(AZH_ERR_ARGUMENT, "hip: board size " + std::to_string(c->board) + " not supported (5, 9, 13, 19)");
+    if (c->history < 1 || c->blocks < 0 || c->filters < 1 || c->value_hidden < 1)
+        throw Error(AZH_ERR_ARGUMENT, "hip: invalid network config");
+    if (c->value_hidden > 256) throw Error(AZH_ERR_ARGUMENT, "hip: value_hidden above 256 not supported");
+    if (c->ownership)
+        throw Error(AZH_ERR_ARGUMENT, "hip: the ownership head is not part of this backend's pass");
+}
+
+// Network::params() then Network::buffers() (src/network.cpp:113-165).
+struct TensorSpec {
+    std::string name;
+    size_t size;
+};
+std::vector<TensorSpec> tensorSpec(const azh_netcfg& c) {
+    const Shape s(c);
+    const size_t F = s.F;
+    std::vector<TensorSpec> t;
+    auto bn = [&](const std::string& p, size_t ch) {
+        t.push_back({p + ".gamma", ch});
+        t.push_back({p + ".beta", ch});
+    };
+    t.push_back({"stem.conv.w", F * s.P * 9});
+    bn("stem.bn", F);
+    for (int i = 0; i < s.blocks; ++i) {
+        const std::string p = "block" + std::to_string(i);
+        t.push_back({p + ".conv1.w", F * F * 9});
+        bn(p + ".bn1", F);
+        t.push_back({p + ".conv2.w", F * F * 9});
+        bn(p + ".bn2", F);
+    }
+    t.push_back({"policy.conv.w", 2 * F});
+    bn("policy.bn", 2);
+    t.push_back({"policy.fc.w", (size_t)2 * s.A * s.A1});
+    t.push_back({"policy.fc.b", (size_t)s.A1});
+    t.push_back({"value.conv.w", F});
+    bn("value.bn", 1);
+    t.push_back({"value.fc1.w", (size_t)s.A * s.V});
+    t.push_back({"value.fc1.b", (size_t)s.V});
+    t.push_back({"value.fc2.w", (size_t)s.V});
+    t.push_back({"value.fc2.b", 1});
+    auto stats = [&](const std::string& p, size_t ch) {
+        t.push_back({p + ".runMean", ch});
+        t.push_back({p + ".runVar", ch});
+    };
+    stats("stem.bn", F);
+    for (int i = 0; i < s.blocks; ++i) {
+        const std::string p = "block" + std::to_string(i);
+        stats(p + ".bn1", F);
+        stats(p + ".bn2", F);
+    }
+    stats("policy.bn", 2);
+    stats("value.bn", 1);
+    return t;
+}
+
+// ---------------------------------------------------------------- weights
+
+struct ConvW {
+    const float* w;   // packed MFMA fragments
+    const float* scale;
+    const float* shift;
+};
+
+struct DeviceWeights {
+    float* arena = nullptr;
+    size_t bytes = 0;
+    ConvW stem{};
+    std::vector<ConvW> conv1, conv2;
+    azh::HeadWeights heads{};
+    ~DeviceWeights() {
+        if (arena) (void)hipFree(arena);
+    }
+};
+
+size_t alignFloats(size_t f) { return (f + 63) / 64 * 64; }   // 256-byte offsets
+
+size_t weightFloats(const azh_netcfg& c) {
+    const Shape s(c);
+    size_t f = 0;
+    f += alignFloats(azh::packedConv3x3Floats(s.P, s.F)) + 2 * alignFloats(s.F);
+    f += (size_t)s.blocks * 2 * (alignFloats(azh::packedConv3x3Floats(s.F, s.F)) + 2 * alignFloats(s.F));
+    f += alignFloats(3 * s.F) + 2 * alignFloats(3);
+    f += alignFloats((size_t)2 * s.A * s.A1) + alignFloats(s.A1);
+    f += alignFloats((size_t)s.A * s.V) + alignFloats(s.V) + alignFloats(s.V) + alignFloats(1);
+    return f;
+}
+
+// BatchNorm2d::forwardInfer's fold (src/layers.cpp:91-92), in float with
+// each operation rounded on its own.
+void foldBn(const float* gamma, const float* beta, const float* mean, const float* var, int C, float* scale,
+            float* shift) {
+    for (int ch = 0; ch < C; ++ch) {
+        scale[ch] = gamma[ch] / std::sqrt(var[ch] + 1e-5f);
+        shift[ch] = beta[ch] - scale[ch] * mean[ch];
+    }
+}
+
+// Checks the tensors against the spec (CudaWeights::upload's contract,
+// src/cuda/cuda_network.cu:24-41, 71-106): exactly the network's tensors, each
+// once, with its size. Host-only, so it runs before any device work.
+std::map<std::string, const float*> checkTensors(const azh_netcfg& c, const azh_tensor* tensors, int count) {
+    const std::vector<TensorSpec> spec = tensorSpec(c);
+    std::map<std::string, const float*> given;
+    if (count < 0 || (count > 0 && !tensors)) throw Error(AZH_ERR_ARGUMENT, "hip: no tensors");
+    for (int i = 0; i < count; ++i) {
+        const azh_tensor& t = tensors[i];
+        if (!t.name) throw Error(AZH_ERR_TENSOR, "hip: a tensor without a name");
+        const std::string name = t.name;
+        const auto it = std::find_if(spec.begin(), spec.end(), [&](const TensorSpec& x) { return x.name == name; });
+        if (it == spec.end())
+            throw Error(AZH_ERR_TENSOR, "hip: tensor '" + name + "' is not read by this backend's pass");
+        if (t.size != it->size)
+            throw Error(AZH_ERR_TENSOR, "hip: tensor '" + name + "' has " + std::to_string(t.size) +
+                                            " floats, expected " + std::to_string(it->size));
+        if (!t.data) throw Error(AZH_ERR_TENSOR, "hip: tensor '" + name + "' has no data");
+        if (!given.emplace(name, t.data).second)
+            throw Error(AZH_ERR_TENSOR, "hip: tensor '" + name + "' given twice");
+    }
+    for (const TensorSpec& x : spec)
+        if (!given.count(x.name)) throw Error(AZH_ERR_TENSOR, "hip: tensor '" + x.name + "' missing");
+    return given;
+}
+
+// Packs, folds and uploads checked tensors into one device arena.
+void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*>& given, DeviceWeights& dw) {
+    const Shape s(c);
+    auto T = [&](const std::string& name) { return given.at(name); };
+
+    std::vector<float> host(weightFloats(c), 0.0f);
+    size_t off = 0;
+    auto take = [&](size_t floats) {
+        const size_t o = off;
+        off += alignFloats(floats);
+        return o;
+    };
+    struct ConvOff {
+        size_t w, scale, shift;
+    };
+    auto conv = [&](const std::string& wname, const std::string& bn, int cin) {
+        ConvOff o;
+        const std::vector<float> packed = azh::packConv3x3(T(wname), cin, s.F);
+        o.w = take(packed.size());
+        std::copy(packed.begin(), packed.end(), host.begin() + o.w);
+        o.scale = take(s.F);
+        o.shift = take(s.F);
+        foldBn(T(bn + ".gamma"), T(bn + ".beta"), T(bn + ".runMean"), T(bn + ".runVar"), s.F, &host[o.scale],
+               &host[o.shift]);
+        return o;
+    };
+    const ConvOff stem = conv("stem.conv.w", "stem.bn", s.P);
+    std::vector<ConvOff> c1, c2;
+    for (int i = 0; i < s.blocks; ++i) {
+        const std::string p = "block" + std::to_string(i);
+        c1.push_back(conv(p + ".conv1.w", p + ".bn1", s.F));
+        c2.push_back(conv(p + ".conv2.w", p + ".bn2", s.F));
+    }
+    const size_t hConv = take(3 * s.F), hScale = take(3), hShift = take(3);
+    std::copy(T("policy.conv.w"), T("policy.conv.w") + 2 * s.F, host.begin() + hConv);
+    std::copy(T("value.conv.w"), T("value.conv.w") + s.F, host.begin() + hConv + 2 * s.F);
+    foldBn(T("policy.bn.gamma"), T("policy.bn.beta"), T("policy.bn.runMean"), T("policy.bn.runVar"), 2,
+           &host[hScale], &host[hShift]);
+    foldBn(T("value.bn.gamma"), T("value.bn.beta"), T("value.bn.runMean"), T("value.bn.runVar"), 1,
+           &host[hScale + 2], &host[hShift + 2]);
+    const size_t pW = take((size_t)2 * s.A * s.A1), pB = take(s.A1);
+    const float* pw = T("policy.fc.w");   // [A+1][2A]
+    for (int a = 0; a < s.A1; ++a)
+        for (int i = 0; i < 2 * s.A; ++i) host[pW + (size_t)i * s.A1 + a] = pw[(size_t)a * 2 * s.A + i];
+    std::copy(T("policy.fc.b"), T("policy.fc.b") + s.A1, host.begin() + pB);
+    const size_t f1W = take((size_t)s.A * s.V), f1B = take(s.V), f2W = take(s.V), f2B = take(1);
+    const float* w1 = T("value.fc1.w");   // [V][A]
+    for (int v = 0; v < s.V; ++v)
+        for (int p = 0; p < s.A; ++p) host[f1W + (size_t)p * s.V + v] = w1[(size_t)v * s.A + p];
+    std::copy(T("value.fc1.b"), T("value.fc1.b") + s.V, host.begin() + f1B);
+    std::copy(T("value.fc2.w"), T("value.fc2.w") + s.V, host.begin() + f2W);
+    host[f2B] = T("value.fc2.b")[0];
+
+    dw.bytes = host.size() * sizeof(float);
+    check(hipMalloc(&dw.arena, dw.bytes), "hipMalloc(weights)");
+    check(hipMemcpy(dw.arena, host.data(), dw.bytes, hipMemcpyHostToDevice), "hipMemcpy(weights)");
+    const float* base = dw.arena;
+    auto mk = [&](const ConvOff& o) { return ConvW{base + o.w, base + o.scale, base + o.shift}; };
+    dw.stem = mk(stem);
+    for (int i = 0; i < s.blocks; ++i) {
+        dw.conv1.push_back(mk(c1[i]));
+        dw.conv2.push_back(mk(c2[i]));
+    }
+    dw.heads = azh::HeadWeights{base + hConv, base + hScale, base + hShift, base + pW, base + pB,
+                                base + f1W,   base + f1B,    base + f2W,    base + f2B};
+}
+
+// ---------------------------------------------------------------- slots
+
+size_t slotFloats(const Shape& s, int maxBatch) {
+    const size_t B = maxBatch;
+    return alignFloats(B * s.P * s.A) + 2 * alignFloats(B * s.F * s.A) + alignFloats(B * s.A1) + alignFloats(B);
+}
+
+size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
+    return (size_t)slots * slotFloats(Shape(c), maxBatch) * sizeof(float) + weightFloats(c) * sizeof(float);
+}
+
+struct Slot {
+    hipStream_t stream = nullptr;
+    hipEvent_t event = nullptr;
+    float* dev = nullptr;
+    float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dLogits = nullptr, *dValues = nullptr;
+    float *hIn = nullptr, *hLogits = nullptr, *hValues = nullptr;
+    std::map<int, hipGraphExec_t> graphs;
+    bool busy = false;
+
+    Slot(const Shape& s, int maxBatch) {
+        const size_t B = maxBatch;
+        check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        check(hipEventCreateWithFlags(&event, hipEventDisableTiming), "hipEventCreate");
+        check(hipMalloc(&dev, slotFloats(s, maxBatch) * sizeof(float)), "hipMalloc(workspace)");
+        size_t off = 0;
+        auto take = [&](size_t f) {
+            float* p = dev + off;
+            off += alignFloats(f);
+            return p;
+        };
+        dIn = take(B * s.P * s.A);
+        dX = take(B * s.F * s.A);
+        dMid = take(B * s.F * s.A);
+        dLogits = take(B * s.A1);
+        dValues = take(B);
+        check(hipHostMalloc((void**)&hIn, B * s.P * s.A * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
+        check(hipHostMalloc((void**)&hLogits, B * s.A1 * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
+        check(hipHostMalloc((void**)&hValues, B * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
+        std::fill(hIn, hIn + B * s.P * s.A, 0.0f);
+    }
+    ~Slot() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
+        if (event) (void)hipEventDestroy(event);
+        if (stream) (void)hipStreamDestroy(stream);
+        if (dev) (void)hipFree(dev);
+        if (hIn) (void)hipHostFree(hIn);
+        if (hLogits) (void)hipHostFree(hLogits);
+        if (hValues) (void)hipHostFree(hValues);
+    }
+};
+
+double freeForCheck() {
+    const size_t limit = gMemoryLimit.load();
+    if (limit > 0) return (double)limit;
+    size_t freeBytes = 0, total = 0;
+    check(hipMemGetInfo(&freeBytes, &total), "hipMemGetInfo");
+    return freeBytes > kMemoryMargin ? (double)(freeBytes - kMemoryMargin) : 0.0;
+}
+
+// checkFits (src/cuda/cuda_runner.cu:206-223), with its message.
+void checkFits(double need, int maxBatch, int hubs) {
+    const double have = freeForCheck();
+    if (need <= have) return;
+    throw Error(AZH_ERR_MEMORY, "hip: inference needs " + std::to_string((long long)(need / 1e6)) +
+                                    " MB of GPU memory at inference_batch " + std::to_string(maxBatch) +
+                                    (hubs > 1 ? " (" + std::to_string(hubs) + " hubs)" : std::string()) +
+                                    ", more than the " + std::to_string((long long)(have / 1e6)) +
+                                    " MB the GPU has free; lower inference_batch");
+}
+
+template <class Body>
+float timeOnStream(hipStream_t stream, int iters, Body body) {
+    hipEvent_t a = nullptr, b = nullptr;
+    check(hipEventCreate(&a), "hipEventCreate");
+    check(hipEventCreate(&b), "hipEventCreate");
+    float ms = 0.0f;
+    try {
+        check(hipEventRecord(a, stream), "hipEventRecord");
+        for (int i = 0; i < iters; ++i) body();
+        check(hipEventRecord(b, stream), "hipEventRecord");
+        check(hipEventSynchronize(b), "hipEventSynchronize");
+        check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+    } catch (...) {
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        throw;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return ms;
+}
+
+} // namespace
+
+// ---------------------------------------------------------------- the runner
+
+struct azh_runner {
+    azh_netcfg cfg{};
+    Shape shape;
+    int maxBatch = 0;
+    DeviceWeights weights;
+    std::vector<std::unique_ptr<Slot>> slots;
+    bool graphs = true;
+
+    struct Pass {
+        int slot;
+        azh_done_fn done;
+        void* user;
+        std::string error;
+    };
+    std::mutex mutex;
+    std::condition_variable wake;
+    std::deque<Pass> queue;
+    bool stop = false;
+    std::thread completion;
+
+    azh_runner(const azh_netcfg& c, int mb) : cfg(c), shape(c), maxBatch(mb) {}
+
+    ~azh_runner() {
+        if (completion.joinable()) {
+            {
+                std::lock_guard<std::mutex> lock(mutex);
+                stop = true;
+            }
+            wake.notify_all();
+            completion.join();   // after every pass in flight has been reported
+        }
+        slots.clear();
+    }
+
+    // The pass's kernels on `stream`: stem, `blocksToRun` residual blocks
+    // (the trunk updated in place: the second conv's epilogue reads the skip
+    // at exactly the element it writes), then the heads when asked.
+    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+        const Shape& sh = shape;
+        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
+        check(azh::launchConv3x3(s.dIn, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, s.dX, B,
+                                 sh.n, sh.P, sh.F, true, t, stream),
+              "conv3x3 (stem)");
+        for (int i = 0; i < blocksToRun; ++i) {
+            const ConvW& a = weights.conv1[i];
+            const ConvW& b = weights.conv2[i];
+            check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
+                                     stream),
+                  "conv3x3 (conv1)");
+            check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, t,
+                                     stream),
+                  "conv3x3 (conv2)");
+        }
+        if (heads)
+            check(azh::launchHeads(s.dX, weights.heads, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, stream), "heads");
+    }
+
+    // The device-resident pass: one captured graph per batch size, replayed.
+    void enqueuePass(Slot& s, int B) {
+        if (!graphs) {
+            launchPass(s, B, s.stream, shape.blocks, true);
+            return;
+        }
+        auto it = s.graphs.find(B);
+        if (it == s.graphs.end()) {
+            hipGraph_t g = nullptr;
+            check(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            try {
+                launchPass(s, B, s.stream, shape.blocks, true);
+            } catch (...) {
+                (void)hipStreamEndCapture(s.stream, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            check(hipStreamEndCapture(s.stream, &g), "hipStreamEndCapture");
+            hipGraphExec_t exec = nullptr;
+            const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            check(e, "hipGraphInstantiate");
+            it = s.graphs.emplace(B, exec).first;
+        }
+        check(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
+    }
+
+    void copyIn(Slot& s, int B) {
+        check(hipMemcpyAsync(s.dIn, s.hIn, (size_t)B * shape.P * shape.A * sizeof(float), hipMemcpyHostToDevice,
+                             s.stream),
+              "hipMemcpyAsync(input)");
+    }
+    void copyOut(Slot& s, int B) {
+        const int delayUs = gCopyOutDelayUs.load();
+        if (delayUs > 0) check(azh::launchSpin(1000ull * delayUs, s.stream), "spin");
+        check(hipMemcpyAsync(s.hLogits, s.dLogits, (size_t)B * shape.A1 * sizeof(float), hipMemcpyDeviceToHost,
+                             s.stream),
+              "hipMemcpyAsync(logits)");
+        check(hipMemcpyAsync(s.hValues, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync(values)");
+    }
+
+    static hipError_t waitFor(hipEvent_t e) {
+        int sleepUs = kPollFirstUs;
+        for (;;) {
+            const hipError_t r = hipEventQuery(e);
+            if (r != hipErrorNotReady) return r;
+            std::this_thread::sleep_for(std::chrono::microseconds(sleepUs));
+            sleepUs = std::min(kPollLastUs, 2 * sleepUs);
+        }
+    }
+
+    void completionLoop() {
+        for (;;) {
+            Pass pass;
+            {
+                std::unique_lock<std::mutex> lock(mutex);
+                wake.wait(lock, [&] { return stop || !queue.empty(); });
+                if (queue.empty()) return;   // stopping, nothing in flight
+                pass = std::move(queue.front());
+                queue.pop_front();
+            }
+            std::string error = pass.error;
+            const hipError_t e = waitFor(slots[pass.slot]->event);
+            if (error.empty() && e != hipSuccess) error = std::string("hip: ") + hipGetErrorString(e);
+            int left = gFailCountdown.load();
+            while (left > 0 && !gFailCountdown.compare_exchange_weak(left, left - 1)) {
+            }
+            if (left == 1 && error.empty()) error = "hip: injected failure (a test hook)";
+            ++gPassesCompleted;
+            {
+                std::lock_guard<std::mutex> lock(mutex);
+                slots[pass.slot]->busy = false;
+            }
+            pass.done(pass.user, pass.slot, error.empty() ? nullptr : error.c_str());
+        }
+    }
+
+    Slot& slotAt(int slot) {
+        if (slot < 0 || slot >= (int)slots.size())
+            throw Error(AZH_ERR_ARGUMENT, "hip: slot " + std::to_string(slot) + " outside [0, " +
+                                              std::to_string(slots.size()) + ")");
+        return *slots[slot];
+    }
+    void checkBatch(int B) const {
+        if (B < 1 || B > maxBatch)
+            throw Error(AZH_ERR_ARGUMENT, "hip: batch of " + std::to_string(B) + " positions outside [1, " +
+                                              std::to_string(maxBatch) + "]");
+    }
+    Slot& idleSlot(int slot) {
+        Slot& s = slotAt(slot);
+        std::lock_guard<std::mutex> lock(mutex);
+        if (s.busy) throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
+        return s;
+    }
+};
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" {
+
+int azh_built(void) { return 1; }
+
+int azh_available(char* why, size_t cap) {
+    Context& c = Context::get();
+    if (!c.ok && why && cap) std::snprintf(why, cap, "%s", c.why.c_str());
+    return c.ok ? 1 : 0;
+}
+
+int azh_describe(char* out, size_t cap) {
+    return guarded([&] {
+        Context& c = Context::get();
+        std::string d;
+        if (!c.ok) {
+            d = c.why;
+        } else {
+            const std::string base = c.arch.substr(0, c.arch.find(':'));
+            char rt[32];
+            std::snprintf(rt, sizeof rt, "%d.%d.%d", c.runtime / 10000000, (c.runtime / 100000) % 100,
+                          c.runtime % 100000);
+            d = c.name + " " + base + ", HIP runtime " + rt + ", kernels " + AZH_KERNEL_HASH;
+        }
+        if (out && cap) std::snprintf(out, cap, "%s", d.c_str());
+    });
+}
+
+const char* azh_last_error(void) { return gLastError.c_str(); }
+
+int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* bytes) {
+    return guarded([&] {
+        validate(cfg);
+        if (max_batch < 1 || slots < 1 || !bytes) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        *bytes = runnerBytes(*cfg, max_batch, slots);
+    });
+}
+
+int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_per_hub) {
+    return guarded([&] {
+        validate(cfg);
+        if (max_batch < 1 || hubs < 1 || slots_per_hub < 1)
+            throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: bad arguments");
+        requireContext();
+        checkFits((double)hubs * runnerBytes(*cfg, max_batch, slots_per_hub), max_batch, hubs);
+    });
+}
+
+int azh_create(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
+               azh_runner** out) {
+    return guarded([&] {
+        if (!out) throw Error(AZH_ERR_ARGUMENT, "hip: no output handle");
+        *out = nullptr;
+        validate(cfg);
+        if (max_batch < 1) throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: maxBatch must be >= 1");
+        if (slots < 1 || slots > kMaxSlots)
+            throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: slots must be in [1, " + std::to_string(kMaxSlots) + "]");
+        const std::map<std::string, const float*> given = checkTensors(*cfg, tensors, count);
+        requireContext();
+        checkFits((double)runnerBytes(*cfg, max_batch, slots), max_batch, 1);
+        std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
+        uploadWeights(*cfg, given, r->weights);
+        for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
+        azh_runner* raw = r.get();
+        r->completion = std::thread([raw] { raw->completionLoop(); });
+        *out = r.release();
+    });
+}
+
+void azh_destroy(azh_runner* r) { delete r; }
+
+int azh_slots(const azh_runner* r) { return r ? (int)r->slots.size() : 0; }
+int azh_max_batch(const azh_runner* r) { return r ? r->maxBatch : 0; }
+
+float* azh_slot_input(azh_runner* r, int slot) {
+    return r && slot >= 0 && slot < (int)r->slots.size() ? r->slots[slot]->hIn : nullptr;
+}
+const float* azh_slot_logits(const azh_runner* r, int slot) {
+    return r && slot >= 0 && slot < (int)r->slots.size() ? r->slots[slot]->hLogits : nullptr;
+}
+const float* azh_slot_values(const azh_runner* r, int slot) {
+    return r && slot >= 0 && slot < (int)r->slots.size() ? r->slots[slot]->hValues : nullptr;
+}
+
+int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user) {
+    return guarded([&] {
+        if (!r || !done) throw Error(AZH_ERR_ARGUMENT, "hip: begin needs a runner and a done callback");
+        r->checkBatch(B);
+        Slot& s = r->slotAt(slot);
+        {
+            std::lock_guard<std::mutex> lock(r->mutex);
+            if (s.busy) throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
+            s.busy = true;
+        }
+        // From here done is called exactly once: errors while enqueueing
+        // travel through it, as a failed pass.
+        std::string error;
+        try {
+            r->copyIn(s, B);
+            r->enqueuePass(s, B);
+            r->copyOut(s, B);
+            check(hipEventRecord(s.event, s.stream), "hipEventRecord");
+        } catch (const std::exception& e) {
+            error = e.what();
+            if (error.empty()) error = "hip: enqueue failed";
+            (void)hipEventRecord(s.event, s.stream);
+        }
+        {
+            std::lock_guard<std::mutex> lock(r->mutex);
+            r->queue.push_back(azh_runner::Pass{slot, done, user, std::move(error)});
+        }
+        r->wake.notify_all();
+    });
+}
+
+int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values) {
+    return guarded([&] {
+        if (!r || !input || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: infer needs its arrays");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(0);
+        std::memcpy(s.hIn, input, (size_t)B * r->shape.P * r->shape.A * sizeof(float));
+        r->copyIn(s, B);
+        r->enqueuePass(s, B);
+        r->copyOut(s, B);
+        check(hipStreamSynchronize(s.stream), "GPU inference failed");
+        std::memcpy(logits, s.hLogits, (size_t)B * r->shape.A1 * sizeof(float));
+        std::memcpy(values, s.hValues, (size_t)B * sizeof(float));
+    });
+}
+
+int azh_softmax_legal(const float* logits, const uint8_t* legal, int B, int actions, float* priors) {
+    return guarded([&] {
+        if (B < 0 || actions < 1 || (B > 0 && (!logits || !legal || !priors)))
+            throw Error(AZH_ERR_ARGUMENT, "hip: softmax needs its arrays");
+        if (B == 0) return;
+        requireContext();
+        const size_t n = (size_t)B * actions;
+        float *dl = nullptr, *dp = nullptr;
+        uint8_t* dm = nullptr;
+        struct Free {
+            void* p[3];
+            ~Free() {
+                for (void* x : p)
+                    if (x) (void)hipFree(x);
+            }
+        } guard{{nullptr, nullptr, nullptr}};
+        check(hipMalloc(&dl, n * sizeof(float)), "hipMalloc");
+        guard.p[0] = dl;
+        check(hipMalloc(&dp, n * sizeof(float)), "hipMalloc");
+        guard.p[1] = dp;
+        check(hipMalloc(&dm, n), "hipMalloc");
+        guard.p[2] = dm;
+        check(hipMemcpy(dl, logits, n * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dm, legal, n, hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchSoftmaxLegal(dl, dm, dp, B, actions, nullptr), "softmax");
+        check(hipMemcpy(priors, dp, n * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+int azh_set_graphs(azh_runner* r, int enabled) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        r->graphs = enabled != 0;
+    });
+}
+
+int azh_stage(azh_runner* r, int slot, int B) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        r->copyIn(s, B);
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+int azh_enqueue(azh_runner* r, int slot, int B) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        r->checkBatch(B);
+        r->enqueuePass(r->idleSlot(slot), B);
+    });
+}
+
+int azh_synchronize(azh_runner* r, int slot) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        check(hipStreamSynchronize(r->slotAt(slot).stream), "hipStreamSynchronize");
+    });
+}
+
+int azh_fetch(azh_runner* r, int slot, int B) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        check(hipMemcpyAsync(s.hLogits, s.dLogits, (size_t)B * r->shape.A1 * sizeof(float),
+                             hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync");
+        check(hipMemcpyAsync(s.hValues, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync");
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+
+int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms) {
+    return guarded([&] {
+        if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        *ms = timeOnStream(s.stream, iters, [&] { r->enqueuePass(s, B); });
+    });
+}
+
+int azh_time_trunk_conv(azh_runner* r, int slot, int B, int iters, float* ms) {
+    return guarded([&] {
+        if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        const Shape& sh = r->shape;
+        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
+        const ConvW& w = r->weights.conv1[0];
+        *ms = timeOnStream(s.stream, iters, [&] {
+            check(azh::launchConv3x3(s.dX, w.w, w.scale, w.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
+                                     s.stream),
+                  "conv3x3");
+        });
+    });
+}
+
+int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms) {
+    return guarded([&] {
+        if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) {
+            r->copyIn(s, B);
+            r->enqueuePass(s, B);
+            r->copyOut(s, B);
+            check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+        }
+        *ms = (float)std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    });
+}
+
+int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const float* shift, const float* skip,
+                      int relu, int B, int n, int cin, int cout, int tiling, float* y) {
+    return guarded([&] {
+        if (!x || !w || !scale || !shift || !y || B < 1 || cin < 1 || cout < 1)
+            throw Error(AZH_ERR_ARGUMENT, "hip: bad conv probe arguments");
+        if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
+        static const azh::ConvTiling table[] = {{2, 4}, {2, 2}, {1, 4}, {1, 2}, {1, 1}};
+        if (tiling < -1 || tiling > 4) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index outside [-1, 4]");
+        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : table[tiling];
+        requireContext();
+        const size_t A = (size_t)n * n;
+        const std::vector<float> packed = azh::packConv3x3(w, cin, cout);
+        const size_t fx = B * cin * A, fy = B * cout * A;
+        std::vector<float*> bufs;
+        auto dev = [&](size_t floats) {
+            float* p = nullptr;
+            check(hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float)), "hipMalloc");
+            bufs.push_back(p);
+            return p;
+        };
+        struct Free {
+            std::vector<float*>& b;
+            ~Free() {
+                for (float* p : b) (void)hipFree(p);
+            }
+        } guard{bufs};
+        float* dx = dev(fx);
+        float* dw = dev(packed.size());
+        float* ds = dev(cout);
+        float* dh = dev(cout);
+        float* dy = dev(fy);
+        float* dk = skip ? dev(fy) : nullptr;
+        check(hipMemcpy(dx, x, fx * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dw, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(ds, scale, cout * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dh, shift, cout * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        if (dk) check(hipMemcpy(dk, skip, fy * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchConv3x3(dx, dw, ds, dh, dk, dy, B, n, cin, cout, relu != 0, t, nullptr), "conv3x3");
+        check(hipMemcpy(y, dy, fy * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values) {
+    return guarded([&] {
+        if (!r || !trunk || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: bad heads probe arguments");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(0);
+        const Shape& sh = r->shape;
+        check(hipMemcpyAsync(s.dX, trunk, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
+              "hipMemcpyAsync");
+        check(azh::launchHeads(s.dX, r->weights.heads, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, s.stream), "heads");
+        check(hipMemcpyAsync(logits, s.dLogits, (size_t)B * sh.A1 * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync");
+        check(hipMemcpyAsync(values, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync");
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+int azh_probe_trunk(azh_runner* r, const float* input, int B, int blocks, float* trunk) {
+    return guarded([&] {
+        if (!r || !input || !trunk) throw Error(AZH_ERR_ARGUMENT, "hip: bad trunk probe arguments");
+        if (blocks < 0 || blocks > r->shape.blocks) throw Error(AZH_ERR_ARGUMENT, "hip: blocks outside the network");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(0);
+        const Shape& sh = r->shape;
+        check(hipMemcpyAsync(s.dIn, input, (size_t)B * sh.P * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
+              "hipMemcpyAsync");
+        r->launchPass(s, B, s.stream, blocks, false);
+        check(hipMemcpyAsync(trunk, s.dX, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync");
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+int azh_probe_fill(float* data, size_t n, float value, size_t tail) {
+    return guarded([&] {
+        if (!data) throw Error(AZH_ERR_ARGUMENT, "hip: no data");
+        requireContext();
+        float* d = nullptr;
+        const size_t total = n + tail;
+        check(hipMalloc(&d, std::max<size_t>(total, 1) * sizeof(float)), "hipMalloc");
+        hipError_t e = hipMemcpy(d, data, total * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = azh::launchFill(d, n, value, nullptr);
+        if (e == hipSuccess) e = hipMemcpy(data, d, total * sizeof(float), hipMemcpyDeviceToHost);
+        (void)hipFree(d);
+        check(e, "fill");
+    });
+}
+
+int azh_probe_copy(size_t bytes, int iters, float* ms) {
+    return guarded([&] {
+        if (!ms || iters < 1 || bytes == 0) throw Error(AZH_ERR_ARGUMENT, "hip: bad copy probe arguments");
+        requireContext();
+        void *a = nullptr, *b = nullptr;
+        check(hipMalloc(&a, bytes), "hipMalloc");
+        hipError_t e = hipMalloc(&b, bytes);
+        if (e != hipSuccess) {
+            (void)hipFree(a);
+            check(e, "hipMalloc");
+        }
+        hipStream_t st = nullptr;
+        e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipMemsetAsync(a, 0, bytes, st);
+        float t = 0.0f;
+        if (e == hipSuccess) {
+            try {
+                t = timeOnStream(st, iters,
+                                 [&] { check(hipMemcpyAsync(b, a, bytes, hipMemcpyDeviceToDevice, st), "copy"); });
+            } catch (const Error& err) {
+                e = hipErrorUnknown;
+                gLastError = err.what();
+            }
+        }
+        if (st) (void)hipStreamDestroy(st);
+        (void)hipFree(a);
+        (void)hipFree(b);
+        check(e, "copy probe");
+        *ms = t;
+    });
+}
+
+void azh_set_hub_chaos_seed(uint64_t seed) { gHubChaosSeed = seed; }
+uint64_t azh_hub_chaos_seed(void) { return gHubChaosSeed.load(); }
+void azh_fail_passes_after(int n) { gFailCountdown = n > 0 ? n + 1 : 0; }
+void azh_set_memory_limit(size_t bytes) { gMemoryLimit = bytes; }
+long long azh_passes_completed(void) { return gPassesCompleted.load(); }
+void azh_set_copy_out_delay(int microseconds) { gCopyOutDelayUs = microseconds > 0 ? microseconds : 0; }
+
+} // extern "C"

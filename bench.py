@@ -1,0 +1,192 @@
+"""Benchmark: positions/s of the inference pass on one MI355X.
+
+A step is one forward pass of the network over one batch of synthetic
+positions already resident in HBM (the pass replayed as its captured
+hipGraph on one stream). Default workload: 19x19, 10 residual blocks of 128
+filters, batch 256 (the headline configuration). Prints one JSON line:
+throughput, the dominant kernel's roofline (the residual-tower 3x3
+convolution, timed live with HIP events on its stream), and the CPU
+baseline (the oracle's single-threaded blas pass, one worker per host core
+at batch 8, as the reference bench's "cpu (blas)" row).
+
+  python bench.py [--steps K] [--warmup W] [--workload 3] [--no-cpu]
+
+Runs on one GPU only: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "alphazero-go_amd")
+sys.path.insert(0, PKG)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3     # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0
+# The reference's published rate for this metric: CUDA fused kernels, 19x19
+# 10x128 batch 256, 2 slots kept full, RTX 4070 Ti SUPER
+# (docs/results/cuda-bench.txt:290).
+REFERENCE_POS_PER_S = 6724.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--batch", type=int, default=0, help="override the workload's batch")
+    ap.add_argument("--conv-iters", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-calls", type=int, default=16, help="batch-8 passes per CPU worker")
+    return ap.parse_args()
+
+
+def traffic_from_profile(workload_name, kernel_hash):
+    """HBM bytes per launch of the tower convolution, from the committed
+    rocprofv3 counter summary of the same kernels, or None."""
+    path = os.path.join(ROOT, "profiles", "conv3x3_tower_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line and not line.startswith("#"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = v.strip()
+    if vals.get("kernels") != kernel_hash or vals.get("workload") != workload_name:
+        return None
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(workload, calls):
+    """The oracle's blas pass (im2col + single-threaded OpenBLAS sgemm, the
+    reference's CPU backend restated) on this host: one worker per core, each
+    running `calls` passes of batch 8, plus one batch-256 pass on one worker."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    w = O.WORKLOADS[workload]
+    net = O.init_network(w.cfg)
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    workers = max(1, min(16, cores))
+    inp8, _ = O.workload_inputs(w, 8)
+    rate, elapsed = O.time_workers(net, inp8, workers, calls, O.BLAS)
+    one_b = min(w.batch, 256)
+    inp_one, _ = O.workload_inputs(w, one_b)
+    rate_one, el_one = O.time_workers(net, inp_one, 1, 1, O.BLAS, warm=False)
+    return {
+        "value": round(rate, 2),
+        "unit": "positions/s",
+        "cores": workers,
+        "kind": "port",
+        "sample": f"{workers} workers x {calls} passes of batch 8 ({workers * calls * 8} positions, "
+                  f"{elapsed:.1f} s); oracle blas restatement of Network::infer",
+        "single_worker_batch": one_b,
+        "single_worker_seconds": round(el_one, 2),
+        "single_worker_value": round(rate_one, 2),
+        "blas": O.blas_description(),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: runs on one GPU only (asked for {args.gpus}); inference of independent "
+              f"positions shards with no exchange step, one runner per GPU", file=sys.stderr)
+        sys.exit(2)
+
+    import azgo_hip
+    import workload as W
+
+    ok, why = azgo_hip.available()
+    if not ok:
+        raise SystemExit(f"bench.py: no usable gfx950 GPU: {why}")
+    w = W.WORKLOADS[args.workload]
+    B = args.batch or w.batch
+    n, H, blocks, F, V = w.cfg
+    tensors = W.network_tensors(w.cfg)
+    inp, _ = W.positions(w, B)
+    cfg = azgo_hip.net_cfg(*w.cfg)
+
+    with azgo_hip.Runner(cfg, tensors, B, 1) as r:
+        r.input(0)[:B] = inp
+        r.stage(0, B)
+        for _ in range(args.warmup):
+            r.enqueue(0, B)
+        r.synchronize(0)
+
+        # The timed region: K passes, synchronized on both sides.
+        r.synchronize(0)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            r.enqueue(0, B)
+        r.synchronize(0)
+        dt = time.perf_counter() - t0
+        ms_per_step = dt * 1e3 / args.steps
+        value = B * args.steps / dt
+
+        # The same passes timed with HIP events on the pass's stream.
+        ev_ms = r.time_passes(0, B, args.steps) / args.steps
+        # The dominant kernel alone: the residual-tower 3x3 convolution.
+        conv_ms = r.time_trunk_conv(0, B, args.conv_iters) / args.conv_iters
+        # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
+        rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
+        logits, values = r.fetch(0, B)
+        assert (logits == logits).all() and (values == values).all(), "NaN in outputs"
+
+    conv_flops = w.trunk_conv_flops(B)
+    achieved = conv_flops / (conv_ms * 1e-3) / 1e12
+    pass_tflops = w.flops_per_position() * B / (ms_per_step * 1e-3) / 1e12
+    kernel_hash = azgo_hip.describe().rsplit("kernels ", 1)[-1]
+    traffic = traffic_from_profile(w.name, kernel_hash)
+
+    line = {
+        "metric": "net evals (positions)/sec at 19x19 batch 256; % fp32-MFMA peak",
+        "value": round(value, 1),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REFERENCE_POS_PER_S, 3) if args.workload == 3 and B == 256 else None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded He-normal weights, synthetic BN statistics, random boards)",
+        "config": {"workload": w.name, "board": n, "blocks": blocks, "filters": F, "value_hidden": V,
+                   "global_batch": B, "parallelism": "single GPU"},
+        "pct_fp32_mfma_peak": round(100 * pass_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
+        "pass_tflops": round(pass_tflops, 2),
+        "event_ms_per_step": round(ev_ms, 4),
+        "round_trip_ms": round(rt_ms, 4),
+        "roofline": {
+            "kernel": "conv3x3 (residual tower, one launch = one layer over the batch)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": traffic,
+            "avg_launch_ms": round(conv_ms, 4),
+            "flops_per_launch": conv_flops,
+        },
+        "device": azgo_hip.describe(),
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(args.workload, args.cpu_calls)
+        line["cpu_baseline"] = cb
+        line["gpu_over_cpu"] = round(value / cb["value"], 1) if cb["value"] > 0 else None
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,217 @@
+/*
+ * azgo_hip.h: the C ABI of the MI355X (gfx950) inference backend for the
+ * residual policy/value network of robominds/alphazero-go.
+ *
+ * This is the drop-in boundary. The reference's GPU plug-in point is the
+ * BatchRunner interface behind its InferenceHub
+ * (include/azgo/inference_hub.hpp:41-53); its CUDA backend implements it in
+ * src/cuda/cuda_runner.cu and exposes the rest through include/azgo/cuda.hpp.
+ * Every entry point below replaces one of those, cited per function. The
+ * thin C++ adapter that a maintainer adds to the reference tree (a
+ * HipBatchRunner deriving from azgo::BatchRunner, makeHipRunner, ...) calls
+ * only these functions.
+ *
+ * Conventions: plain pointers and sizes, no exceptions across the ABI. Every
+ * function returning int returns AZH_OK (0) on success or a negative
+ * AZH_ERR_* code, and then azh_last_error() (per thread) says what failed,
+ * in the reference's wording where it has one ("hip: ...", "lower
+ * inference_batch"). Arrays are fp32, row-major, the reference's layouts:
+ * input [B][2H+2][n*n] (Evaluator::evaluate, include/azgo/evaluator.hpp:24),
+ * logits [B][n*n+1], values [B] (tanh).
+ */
+#ifndef AZGO_HIP_H
+#define AZGO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    AZH_OK = 0,
+    AZH_ERR_ARGUMENT = -1,    /* std::invalid_argument in the reference */
+    AZH_ERR_UNAVAILABLE = -2, /* no usable GPU / wrong architecture */
+    AZH_ERR_MEMORY = -3,      /* std::runtime_error "... lower inference_batch" */
+    AZH_ERR_TENSOR = -4,      /* std::logic_error naming a tensor (upload contract) */
+    AZH_ERR_HIP = -5,         /* a HIP runtime error ("hip: ...") */
+    AZH_ERR_STATE = -6        /* a call the runner's state does not allow */
+};
+
+/* NetConfig (include/azgo/network.hpp:24-36). ownership must be 0: the
+ * ownership head is not part of this backend's pass (its tensors would be
+ * refused as unread). */
+typedef struct azh_netcfg {
+    int board;        /* n: 5, 9, 13 or 19 */
+    int history;      /* H: planes = 2H + 2 */
+    int blocks;       /* residual blocks */
+    int filters;      /* F */
+    int value_hidden; /* V, at most 256 */
+    int ownership;
+} azh_netcfg;
+
+/* One named tensor of Network::params() / buffers() (src/network.cpp:113-165),
+ * e.g. "block3.conv2.w", "policy.bn.runVar". */
+typedef struct azh_tensor {
+    const char* name;
+    const float* data;
+    size_t size; /* floats */
+} azh_tensor;
+
+typedef struct azh_runner azh_runner;
+
+/* BatchRunner::begin's done callback (include/azgo/inference_hub.hpp:47-50):
+ * called exactly once per pass, from the runner's completion thread, with
+ * error NULL on success or a message ("hip: ..."). It must only mark and
+ * wake (it may not call back into the runner). */
+typedef void (*azh_done_fn)(void* user, int slot, const char* error);
+
+/* ---------------------------------------------------------------- probes */
+
+/* cudaBuilt (include/azgo/cuda.hpp:29-30): 1 in this library. */
+int azh_built(void);
+
+/* cudaAvailable (include/azgo/cuda.hpp:32-39; src/cuda/cuda_context.cu:32-87):
+ * 1 when a gfx950 device is present and a first kernel ran; else 0 and, when
+ * why is not NULL, the reason (e.g. "kernels built for gfx950; this GPU is
+ * gfx942"). The first call sets up the process-wide HIP context. */
+int azh_available(char* why, size_t cap);
+
+/* cudaDescription (include/azgo/cuda.hpp:41-49): GPU name, gfx arch, HIP
+ * runtime version and a hash of the kernel sources and flags. */
+int azh_describe(char* out, size_t cap);
+
+/* The message of the calling thread's last failed call ("" if none). */
+const char* azh_last_error(void);
+
+/* ---------------------------------------------------------------- runners */
+
+/* checkCudaInferenceMemory / hubBytes (include/azgo/cuda.hpp:60-66;
+ * src/cuda/cuda_runner.cu:186-223): device bytes one runner of `slots` slots
+ * of max_batch positions needs (weights included). */
+int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* bytes);
+
+/* The same check the constructor makes: AZH_ERR_MEMORY with the reference's
+ * message unless `hubs` runners of that shape fit in free memory less
+ * 512 MB (or the test hook's limit). */
+int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_per_hub);
+
+/* makeCudaRunner (include/azgo/cuda.hpp:53-58; src/cuda/cuda_runner.cu:227-234)
+ * and CudaWeights::upload (src/cuda/cuda_network.cu:71-106): checks memory,
+ * uploads the tensors once (the caller's arrays are not kept), allocates
+ * `slots` (1..2) slots of max_batch positions, each with its own stream,
+ * device workspace and pinned staging, and starts the completion thread.
+ * The tensors must be exactly the network's params() and buffers(): an
+ * unknown name, a wrong size, a missing tensor or a tensor this pass never
+ * reads fail with AZH_ERR_TENSOR naming it. */
+int azh_create(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
+               azh_runner** out);
+
+/* Waits for every pass in flight, then frees everything
+ * (CudaBatchRunner::~CudaBatchRunner, src/cuda/cuda_runner.cu:64-71). */
+void azh_destroy(azh_runner* r);
+
+int azh_slots(const azh_runner* r);     /* BatchRunner::slots */
+int azh_max_batch(const azh_runner* r); /* BatchRunner::maxBatch */
+
+/* BatchRunner::input / logits / values (include/azgo/inference_hub.hpp:46-52):
+ * the slot's pinned host staging, [max_batch][planes][area],
+ * [max_batch][area+1], [max_batch]. Outputs are valid after done until the
+ * slot's next begin. NULL for a bad slot. */
+float* azh_slot_input(azh_runner* r, int slot);
+const float* azh_slot_logits(const azh_runner* r, int slot);
+const float* azh_slot_values(const azh_runner* r, int slot);
+
+/* BatchRunner::begin (include/azgo/inference_hub.hpp:47-50;
+ * CudaBatchRunner::begin, src/cuda/cuda_runner.cu:79-105): enqueues copy
+ * in, the pass on the first B positions of the slot's input, copy out and
+ * an event, and returns at once; done(user, slot, error) follows from the
+ * completion thread once the outputs are on the host. A B outside
+ * [1, max_batch] or a busy slot fails here, before anything is enqueued
+ * (the hub turns that into a failed batch). */
+int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user);
+
+/* CudaInference::infer (include/azgo/cuda.hpp:68-84;
+ * src/cuda/cuda_network.cu:314-339): the whole pass synchronously on slot
+ * 0's resources; the slot must be idle. */
+int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values);
+
+/* The legal-move softmax on the GPU (no reference counterpart on the GPU; it
+ * restates Mcts::expand's priors, src/mcts.cpp:170-183): priors[b][a] =
+ * exp(l - max) / sum over legal of the same, 0 where legal[b][a] == 0.
+ * Host arrays [B][actions]; runs on its own stream and waits. */
+int azh_softmax_legal(const float* logits, const uint8_t* legal, int B, int actions, float* priors);
+
+/* Whether passes replay a captured hipGraph per batch size (default 1), or
+ * launch their kernels one by one. */
+int azh_set_graphs(azh_runner* r, int enabled);
+
+/* ---------------------------------------------------------------- device-resident passes (measurement) */
+
+/* Copies the first B positions of the slot's pinned input to its device
+ * buffer and waits. */
+int azh_stage(azh_runner* r, int slot, int B);
+/* Enqueues the pass on the slot's stream over the staged device input, no
+ * host copies (what a timed region measures with the inputs already in HBM). */
+int azh_enqueue(azh_runner* r, int slot, int B);
+/* Waits for the slot's stream. */
+int azh_synchronize(azh_runner* r, int slot);
+/* Copies the slot's device outputs for B positions into its pinned outputs and waits. */
+int azh_fetch(azh_runner* r, int slot, int B);
+/* HIP events on the slot's stream around `iters` device-resident passes:
+ * total milliseconds. */
+int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms);
+/* HIP events on the slot's stream around `iters` launches of the first
+ * residual block's first convolution alone (the dominant kernel): total ms. */
+int azh_time_trunk_conv(azh_runner* r, int slot, int B, int iters, float* ms);
+/* Events around `iters` synchronous round trips: pinned H2D, pass, D2H. */
+int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
+
+/* ---------------------------------------------------------------- kernel probes (tests) */
+
+/* The pass's 3x3 convolution kernel alone (cuda_probe::convBnRelu,
+ * include/azgo/cuda.hpp:123-126): x [B][cin][n*n], w [cout][cin*9],
+ * y [B][cout][n*n] = relu?(scale*conv + shift (+ skip)). skip may be NULL.
+ * tiling: -1 the pass's rule, else an index 0..4 forcing a workgroup shape. */
+int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const float* shift, const float* skip,
+                      int relu, int B, int n, int cin, int cout, int tiling, float* y);
+
+/* The heads kernel alone on the runner's weights: trunk [B][F][n*n] ->
+ * logits, values. */
+int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values);
+
+/* The stem and the first `blocks` residual blocks on the runner's weights:
+ * input [B][planes][n*n] -> trunk [B][F][n*n]. */
+int azh_probe_trunk(azh_runner* r, const float* input, int B, int blocks, float* trunk);
+
+/* cuda_probe::fill (include/azgo/cuda.hpp:101-103): data[0..n) = value on the
+ * GPU; all n + tail floats travel, so a test can see the tail untouched. */
+int azh_probe_fill(float* data, size_t n, float value, size_t tail);
+
+/* A plain device-to-device copy of `bytes` (known traffic, to scale HBM
+ * counters), repeated `iters` times; total ms. */
+int azh_probe_copy(size_t bytes, int iters, float* ms);
+
+/* ---------------------------------------------------------------- test hooks (cuda_probe, include/azgo/cuda.hpp:138-155) */
+
+/* Hub chaos seed WorkerEvaluators reads (cuda_probe::setHubChaosSeed). */
+void azh_set_hub_chaos_seed(uint64_t seed);
+uint64_t azh_hub_chaos_seed(void);
+/* After n more passes complete normally the next one reports a failure
+ * through done (once); 0 disables (cuda_probe::failPassesAfter). */
+void azh_fail_passes_after(int n);
+/* A stand-in for free device memory in the memory checks; 0 restores the
+ * device's (cuda_probe::setMemoryLimit). */
+void azh_set_memory_limit(size_t bytes);
+/* Passes the runners of this process have reported (cuda_probe::passesCompleted). */
+long long azh_passes_completed(void);
+/* Holds each pass's stream this long before its copy-out
+ * (cuda_probe::setCopyOutDelay). */
+void azh_set_copy_out_delay(int microseconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AZGO_HIP_H */

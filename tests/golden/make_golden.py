@@ -1,0 +1,100 @@
+"""Writes the golden vectors under tests/golden/ from the REFERENCE's own code:
+its sources compiled in place into oracle/_ref/libazgo_ref.so by
+oracle/Makefile (naive backend; the reference's BLAS backend needs
+<cblas.h>, which this image lacks). Run where the reference tree is present:
+
+    make -C oracle && python tests/golden/make_golden.py
+
+Vectors (data only, no reference source):
+  rng.json        Rng(seed).next()/uniform()/normal()/below() draws and
+                  deriveSeed values (src/rng.cpp)
+  weights.json    sha256 of every tensor of Network(cfg, 1) for the five
+                  workloads' shapes (src/network.cpp:77-111), params() order
+  encode.npz      encodePlanes outputs (src/encode.cpp:14-43) for fixed
+                  stone patterns under all 8 symmetries
+  infer_*.npz     Network::infer (naive backend) inputs and outputs: the
+                  5x5 4x32 workload (seeded weights, synthetic BN statistics,
+                  batch 8) and a 9x9 2x16 network with random BN and biases
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+import oracle as O  # noqa: E402
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
+
+
+def main():
+    if not O.ref_available():
+        raise SystemExit("oracle/_ref/libazgo_ref.so is not built (make -C oracle with the reference present)")
+    h = O._ref()
+    import ctypes as C
+    rng = {"next": {}, "uniform": {}, "normal": {}, "below7": {}, "derive": []}
+    for seed in (0, 1, 42, 2 ** 63 + 5):
+        out = (C.c_uint64 * 16)()
+        h.ref_rng_next_u64(seed, 16, out)
+        rng["next"][str(seed)] = [str(v) for v in out]
+        for kind, key in ((1, "uniform"), (2, "normal"), (3, "below7")):
+            d = (C.c_double * 16)()
+            h.ref_rng_draws(seed, kind, 7, 16, d)
+            rng[key][str(seed)] = [float(v).hex() for v in d]
+    for args in ((1, 0xB4, 0, 0), (1, 3, 0, 0), (1, 3, 255, 0), (4, 3, 2, 1), (1, 2, 3, 4)):
+        rng["derive"].append([list(args), str(h.ref_derive_seed(*args))])
+    with open(os.path.join(HERE, "rng.json"), "w") as f:
+        json.dump(rng, f, indent=1)
+
+    weights = {}
+    for tag, w in O.WORKLOADS.items():
+        if tag == 4:
+            continue   # the same network as workload 3
+        ref = O.RefNetwork(w.cfg, 1)
+        weights[str(tag)] = {name: sha(ref.get(name)) for name, _, _, _ in ref.layout()}
+    with open(os.path.join(HERE, "weights.json"), "w") as f:
+        json.dump(weights, f, indent=1)
+
+    g = np.random.default_rng(2024)
+    enc = {}
+    for n in (5, 9, 19):
+        stones = g.integers(0, 3, (3, n * n)).astype(np.uint8)   # three plies of history
+        enc[f"stones_{n}"] = stones
+        for to_move in (1, 2):
+            for H in (1, 2, 8):
+                for sym in range(8):
+                    out = np.empty((2 * H + 2) * n * n, np.float32)
+                    h.ref_encode_planes(stones.ctypes.data_as(C.POINTER(C.c_uint8)), 3, n, to_move, H, sym,
+                                        O.fptr(out))
+                    enc[f"planes_{n}_{to_move}_{H}_{sym}"] = out
+    np.savez_compressed(os.path.join(HERE, "encode.npz"), **enc)
+
+    w = O.WORKLOADS[1]
+    net = O.init_network(w.cfg)
+    ref = O.RefNetwork(w.cfg, 1)
+    ref.load(net)
+    inp, legal = O.workload_inputs(w, 8)
+    logits, values = ref.infer(inp)
+    np.savez_compressed(os.path.join(HERE, "infer_5x5_workload.npz"), input=inp, legal=legal, logits=logits,
+                        values=values)
+
+    cfg = O.make_cfg(9, 2, 16, value_hidden=16)
+    net = O.random_network(cfg, 7)
+    ref = O.RefNetwork(cfg, 7)
+    ref.load(net)
+    inp = np.random.default_rng(8).integers(0, 2, (4, cfg.planes, cfg.area)).astype(np.float32)
+    logits, values = ref.infer(inp)
+    tensors = {"t_" + k: v for k, v in net.tensors().items()}
+    np.savez_compressed(os.path.join(HERE, "infer_9x9_random.npz"), input=inp, logits=logits, values=values,
+                        **tensors)
+    print("golden vectors written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,368 @@
+"""Pins the oracle (the CPU restatement of the reference's inference pass)
+before it is trusted as the checker:
+- known answers the reference's own tests hold (splitmix64, encode planes,
+  symmetry images, im2col, the conv and BN hand examples, the gemm beta-0
+  example);
+- the golden vectors of tests/golden/, written by the reference's own code
+  compiled from source (rng draws, weight hashes, encode planes, whole
+  Network::infer outputs), bit for bit;
+- the reference compiled from source (oracle/_ref), when built, bit for bit;
+- mathematics: the published xoshiro256** step, He-normal scale, BN closed
+  forms, double-precision gemm bounds, softmax closed forms.
+All CPU-only.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference tree)")
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------------ rng
+
+def test_splitmix64_known_outputs():
+    """tests/test_rng.cpp:11-18."""
+    x = 0
+    outs = []
+    for _ in range(3):
+        v, x = O.splitmix64(x)
+        outs.append(v)
+    assert outs == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    assert x == (3 * 0x9E3779B97F4A7C15) % 2 ** 64
+
+
+def test_xoshiro_step_by_hand():
+    """The published xoshiro256** output rotl(s1 * 5, 7) * 9 from a hand-set
+    state {1, 2, 3, 4}: 11520 (2*5 = 10, rotl 7 = 1280, * 9)."""
+    r = O.Rng(0)
+    for i, v in enumerate((1, 2, 3, 4)):
+        r.state[i] = v
+    assert r.next() == 11520
+    # The state update of the same step: s2 ^= s0 -> 2, s3 ^= s1 -> 6, s1 ^= s2 -> 0,
+    # s0 ^= s3 -> 7, s2 ^= s1 << 17 -> 2 ^ (2 << 17), s3 = rotl(6, 45).
+    assert list(r.state) == [7, 0, 2 ^ (2 << 17), (6 << 45) % 2 ** 64]
+
+
+def test_rng_matches_golden_vectors():
+    gold = json.load(open(os.path.join(GOLD, "rng.json")))
+    for seed, draws in gold["next"].items():
+        r = O.Rng(int(seed))
+        assert [r.next() for _ in draws] == [int(v) for v in draws]
+    for key, fn in (("uniform", "uniform"), ("normal", "normal")):
+        for seed, draws in gold[key].items():
+            r = O.Rng(int(seed))
+            assert [getattr(r, fn)() for _ in draws] == [float.fromhex(v) for v in draws]
+    for seed, draws in gold["below7"].items():
+        r = O.Rng(int(seed))
+        assert [r.below(7) for _ in draws] == [int(float.fromhex(v)) for v in draws]
+    for args, v in gold["derive"]:
+        assert O.derive_seed(*args) == int(v)
+
+
+def test_uniform_and_normal_statistics():
+    r = O.Rng(3)
+    u = np.array([r.uniform() for _ in range(20000)])
+    assert 0 <= u.min() and u.max() < 1 and abs(u.mean() - 0.5) < 0.01
+    z = np.array([r.normal() for _ in range(20000)])
+    assert abs(z.mean()) < 0.03 and abs(z.std() - 1) < 0.03
+    b = np.array([r.below(7) for _ in range(7000)])
+    assert b.min() == 0 and b.max() == 6 and np.all(np.bincount(b) > 850)
+
+
+# ------------------------------------------------------------------ weights
+
+@pytest.mark.parametrize("tag", [1, 2, 3, 5])
+def test_weights_match_reference_hashes(tag):
+    """Network(cfg, 1)'s tensors, hashed from the reference's own build."""
+    gold = json.load(open(os.path.join(GOLD, "weights.json")))[str(tag)]
+    net = O.init_network(O.WORKLOADS[tag].cfg, synthetic_bn=False)
+    t = net.tensors()
+    assert list(t) == list(gold)
+    for name, h in gold.items():
+        assert hashlib.sha256(np.ascontiguousarray(t[name]).tobytes()).hexdigest() == h, name
+
+
+def test_he_normal_scale():
+    """tests/test_layers.cpp:212-236: std within 10% of sqrt(2/fanIn)."""
+    net = O.init_network(O.make_cfg(9, 2, 64), synthetic_bn=False)
+    for name, t in net.tensors().items():
+        if name.endswith("conv1.w") or name == "policy.fc.w":
+            fan = 64 * 9 if "conv" in name else 2 * 81
+            sd = np.sqrt(2.0 / fan)
+            assert abs(t.std() - sd) <= 0.1 * sd and abs(t.mean()) <= 0.1 * sd
+        if name.endswith(".b") or name.endswith(".beta"):
+            assert np.all(t == 0)
+        if name.endswith(".gamma"):
+            assert np.all(t == 1)
+
+
+def test_synthetic_bn_statistics():
+    cfg = O.WORKLOADS[3].cfg
+    t = O.init_network(cfg).tensors()
+    means = np.concatenate([v for k, v in t.items() if k.endswith("runMean")])
+    var = np.concatenate([v for k, v in t.items() if k.endswith("runVar")])
+    assert abs(means.std() - 0.1) < 0.01 and abs(means.mean()) < 0.01
+    assert var.min() >= 0.5 and var.max() < 1.5 and abs(var.mean() - 1.0) < 0.02
+
+
+def test_param_layout_offsets():
+    """tests/test_network.cpp:762-798: 64-float aligned, ordered, no overlap."""
+    for cfg in (O.make_cfg(9, 2, 16, 8), O.make_cfg(9, 0, 16, 8), O.make_cfg(9, 2, 16, 8, ownership=1)):
+        lay = O.layout(cfg)
+        pf, bf = O.arena_sizes(cfg)
+        for arena, total in ((0, pf), (1, bf)):
+            end = 0
+            for name, size, off, buf in lay:
+                if buf != arena:
+                    continue
+                assert off % 64 == 0 and off >= end
+                end = off + size
+            assert end <= total and total % 64 == 0
+        names = [x[0] for x in lay]
+        assert ("ownership.conv.w" in names) == bool(cfg.ownership)
+
+
+@needs_ref
+@pytest.mark.parametrize("cfg", [O.make_cfg(5, 4, 32), O.make_cfg(9, 2, 16, 8, ownership=1), O.make_cfg(13, 1, 24)])
+def test_layout_and_weights_match_reference_build(cfg):
+    ref = O.RefNetwork(cfg, 5)
+    assert ref.layout() == O.layout(cfg)
+    assert ref.sizes() == O.arena_sizes(cfg)
+    net = O.init_network(cfg, 5, synthetic_bn=False)
+    for name, t in net.tensors().items():
+        assert np.array_equal(_bits(ref.get(name)), _bits(t)), name
+
+
+# ------------------------------------------------------------------ encoding and symmetry
+
+def _pt(r, c, n=5):
+    return r * n + c
+
+
+def _plane_is(planes, k, ones, n=5):
+    want = np.zeros(n * n, np.float32)
+    want[list(ones)] = 1
+    return np.array_equal(planes[k], want)
+
+
+def test_encode_own_opponent_swap():
+    """tests/test_encode.cpp:56-75."""
+    s = np.zeros(25, np.uint8)
+    s[_pt(0, 0)] = 1
+    s[_pt(4, 4)] = 2
+    black = O.encode_planes(s, 5, 1, 1)
+    assert _plane_is(black, 0, [_pt(0, 0)]) and _plane_is(black, 1, [_pt(4, 4)])
+    assert _plane_is(black, 2, range(25)) and _plane_is(black, 3, [])
+    white = O.encode_planes(s, 5, 2, 1)
+    assert _plane_is(white, 0, [_pt(4, 4)]) and _plane_is(white, 1, [_pt(0, 0)])
+    assert _plane_is(white, 2, []) and _plane_is(white, 3, range(25))
+
+
+def test_encode_missing_history_is_zero():
+    """tests/test_encode.cpp:77-93."""
+    s = np.zeros(25, np.uint8)
+    s[_pt(2, 2)] = 1
+    out = O.encode_planes(s, 5, 1, 4)
+    assert out.shape == (10, 25)
+    assert _plane_is(out, 0, [_pt(2, 2)])
+    for k in range(1, 8):
+        assert _plane_is(out, k, [])
+    assert _plane_is(out, 8, range(25)) and _plane_is(out, 9, [])
+    start = O.encode_planes(np.zeros(25, np.uint8), 5, 1, 8)
+    for k in range(16):
+        assert _plane_is(start, k, [])
+    assert _plane_is(start, 16, range(25)) and _plane_is(start, 17, [])
+
+
+def test_encode_game_history():
+    """tests/test_encode.cpp:95-123: B (0,0), W (4,4), B (2,2), White to move;
+    the boards newest first, built by hand (no captures)."""
+    b3 = np.zeros(25, np.uint8)
+    b3[[_pt(0, 0), _pt(2, 2)]] = 1
+    b3[_pt(4, 4)] = 2
+    b2 = np.zeros(25, np.uint8)
+    b2[_pt(0, 0)] = 1
+    b2[_pt(4, 4)] = 2
+    b1 = np.zeros(25, np.uint8)
+    b1[_pt(0, 0)] = 1
+    b0 = np.zeros(25, np.uint8)
+    out = O.encode_planes(np.stack([b3, b2, b1, b0]), 5, 2, 4)
+    assert _plane_is(out, 0, [_pt(4, 4)]) and _plane_is(out, 1, [_pt(0, 0), _pt(2, 2)])
+    assert _plane_is(out, 2, [_pt(4, 4)]) and _plane_is(out, 3, [_pt(0, 0)])
+    assert _plane_is(out, 4, []) and _plane_is(out, 5, [_pt(0, 0)])
+    assert _plane_is(out, 6, []) and _plane_is(out, 7, [])
+    assert _plane_is(out, 8, []) and _plane_is(out, 9, range(25))
+    short = O.encode_planes(np.stack([b3, b2, b1, b0]), 5, 2, 2)
+    assert short.shape == (6, 25)
+    assert _plane_is(short, 2, [_pt(4, 4)]) and _plane_is(short, 3, [_pt(0, 0)]) and _plane_is(short, 5, range(25))
+
+
+def test_symmetry_hand_images():
+    """tests/test_symmetry.cpp:10-39."""
+    n = 5
+    T = O.transform_point
+    assert all(T(0, p, 9) == p for p in range(81))
+    assert T(1, _pt(0, 0), n) == _pt(0, 4) and T(1, _pt(0, 4), n) == _pt(4, 4) and T(1, _pt(0, 1), n) == _pt(1, 4)
+    assert T(2, _pt(0, 1), n) == _pt(4, 3) and T(3, _pt(0, 1), n) == _pt(3, 0)
+    assert T(4, _pt(0, 1), n) == _pt(0, 3) and T(5, _pt(0, 1), n) == _pt(3, 4)
+    assert T(6, _pt(0, 1), n) == _pt(4, 1) and T(7, _pt(0, 1), n) == _pt(1, 0)
+    assert all(T(s, _pt(2, 2), n) == _pt(2, 2) for s in range(8))
+
+
+def test_encode_matches_golden_planes():
+    gold = np.load(os.path.join(GOLD, "encode.npz"))
+    for n in (5, 9, 19):
+        stones = gold[f"stones_{n}"]
+        for to_move in (1, 2):
+            for H in (1, 2, 8):
+                for sym in range(8):
+                    got = O.encode_planes(stones, n, to_move, H, sym).reshape(-1)
+                    assert np.array_equal(got, gold[f"planes_{n}_{to_move}_{H}_{sym}"]), (n, to_move, H, sym)
+
+
+# ------------------------------------------------------------------ layers
+
+def test_im2col_hand_example():
+    """tests/test_backend.cpp:121-138."""
+    img = np.arange(1, 10, dtype=np.float32)
+    col = O.im2col(img, 1, 1, 3, 3).reshape(9, 9)
+    for r in range(9):
+        assert col[r, 4] == img[r] and col[4, r] == img[r]
+    assert col[:, 0].tolist() == [0, 0, 0, 0, 1, 2, 0, 4, 5]
+    assert col[:, 8].tolist() == [5, 6, 0, 8, 9, 0, 0, 0, 0]
+
+
+def test_conv_hand_example():
+    """tests/test_layers.cpp:145-157: all-ones kernel on 1..9."""
+    y = O.conv3x3(np.ones(9, np.float32), 1, 1, np.arange(1, 10, dtype=np.float32), 1, 3)
+    assert y.tolist() == [12, 21, 16, 27, 45, 33, 24, 39, 28]
+
+
+def test_bn_hand_values():
+    """tests/test_layers.cpp:159-171."""
+    eps = np.float32(1e-5)
+    y = O.bn_infer([2, 0.5], [1, -1], [1, -2], [np.float32(4) - eps, np.float32(0.25) - eps],
+                   np.array([1, 3, -1, -2, -1.5, 0], np.float32), 2, 3)
+    assert np.allclose(y, [1, 3, -1, -1, -0.5, 1], atol=1e-5)
+
+
+def test_gemm_beta_zero_ignores_nan():
+    """tests/test_backend.cpp:91-100 (the oracle's gemm always overwrites C)."""
+    A = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    B = np.array([[1, 0], [0, 1], [1, 1]], np.float32)
+    for mode in (O.NAIVE, O.BLAS):
+        assert O.gemm(A, B, mode=mode).tolist() == [[4, 5], [10, 11]]
+
+
+@pytest.mark.parametrize("mode", [O.NAIVE, O.BLAS])
+def test_gemm_vs_double(mode):
+    """tests/test_backend.cpp:36-82: within 1e-4 relative of a double gemm."""
+    g = np.random.default_rng(11)
+    for M, N, K in ((1, 1, 1), (3, 5, 7), (64, 300, 576), (2, 92, 128), (17, 1, 33)):
+        for transB in (False, True):
+            A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+            B = g.uniform(-1, 1, (N, K) if transB else (K, N)).astype(np.float32)
+            ref = A.astype(np.float64) @ (B.T if transB else B).astype(np.float64)
+            got = O.gemm(A, B, transB, mode)
+            assert np.all(np.abs(got - ref) <= 1e-4 * np.maximum(1, np.abs(ref)))
+
+
+# ------------------------------------------------------------------ whole pass
+
+def test_naive_pass_matches_golden_workload():
+    gold = np.load(os.path.join(GOLD, "infer_5x5_workload.npz"))
+    w = O.WORKLOADS[1]
+    net = O.init_network(w.cfg)
+    inp, legal = O.workload_inputs(w, 8)
+    assert np.array_equal(inp, gold["input"]) and np.array_equal(legal, gold["legal"])
+    logits, values = O.forward(net, inp, O.NAIVE)
+    assert np.array_equal(_bits(logits), _bits(gold["logits"])) and np.array_equal(_bits(values), _bits(gold["values"]))
+
+
+def test_naive_pass_matches_golden_random_network():
+    gold = np.load(os.path.join(GOLD, "infer_9x9_random.npz"))
+    cfg = O.make_cfg(9, 2, 16, value_hidden=16)
+    net = O.init_network(cfg, 7, synthetic_bn=False)
+    for name, t in net.tensors().items():
+        t[:] = gold["t_" + name]
+    logits, values = O.forward(net, gold["input"], O.NAIVE)
+    assert np.array_equal(_bits(logits), _bits(gold["logits"])) and np.array_equal(_bits(values), _bits(gold["values"]))
+
+
+@needs_ref
+@pytest.mark.parametrize("cfg,B,seed", [(O.make_cfg(5, 4, 32), 8, 1), (O.make_cfg(9, 6, 64), 4, 1),
+                                        (O.make_cfg(13, 2, 40, value_hidden=20), 3, 9),
+                                        (O.make_cfg(9, 0, 8), 2, 3)])
+def test_naive_pass_matches_reference_build(cfg, B, seed):
+    net = O.random_network(cfg, seed)
+    ref = O.RefNetwork(cfg, seed)
+    ref.load(net)
+    inp = np.random.default_rng(seed).integers(0, 2, (B, cfg.planes, cfg.area)).astype(np.float32)
+    a = ref.infer(inp)
+    b = O.forward(net, inp, O.NAIVE)
+    assert np.array_equal(_bits(a[0]), _bits(b[0])) and np.array_equal(_bits(a[1]), _bits(b[1]))
+
+
+@pytest.mark.parametrize("cfg", [O.make_cfg(5, 2, 8, 8), O.make_cfg(9, 1, 16, 16), O.make_cfg(5, 0, 4, 4)])
+def test_double_pass_vs_float_passes(cfg):
+    """The three passes agree to float noise (maxErr 1e-5, the reference's
+    whole-network ceiling, tests/test_cuda.cpp:756-776)."""
+    net = O.random_network(cfg, 21)
+    inp = np.random.default_rng(22).integers(0, 2, (3, cfg.planes, cfg.area)).astype(np.float32)
+    d = O.forward_double(net, inp)
+    for mode in (O.NAIVE, O.BLAS):
+        f = O.forward(net, inp, mode)
+        assert O.max_err(f[0], d[0]) <= 1e-5 and np.abs(f[1] - d[1]).max() <= 1e-5
+
+
+def test_double_pass_closed_form():
+    """A network whose every weight is zero except the biases: logits are the
+    policy bias, the value tanh(fc2 bias), for any input."""
+    cfg = O.make_cfg(5, 1, 4, 4)
+    net = O.init_network(cfg, 1, synthetic_bn=False)
+    t = net.tensors()
+    for name, v in t.items():
+        if name.endswith(".w"):
+            v[:] = 0
+    t["policy.fc.b"][:] = np.arange(26, dtype=np.float32) / 7
+    t["value.fc2.b"][:] = 0.25
+    inp = np.random.default_rng(1).integers(0, 2, (2, cfg.planes, cfg.area)).astype(np.float32)
+    for fwd in (O.forward_double, lambda n, x: O.forward(n, x, O.NAIVE)):
+        logits, values = fwd(net, inp)
+        assert np.allclose(logits, np.arange(26) / 7, atol=1e-6) and np.allclose(values, np.tanh(0.25), atol=1e-7)
+
+
+def test_softmax_closed_forms():
+    """Mcts::expand's priors (src/mcts.cpp:170-183)."""
+    logits = np.array([[0, np.log(2), np.log(3), 50.0], [1, 2, 3, 4], [5, 5, 5, 5]], np.float32)
+    legal = np.array([[1, 1, 1, 0], [0, 0, 0, 1], [1, 1, 1, 1]], np.uint8)
+    p = O.softmax_legal(logits, legal)
+    assert np.allclose(p[0], [1 / 6, 2 / 6, 3 / 6, 0], atol=1e-7) and p[0, 3] == 0
+    assert p[1].tolist() == [0, 0, 0, 1]
+    assert np.allclose(p[2], 0.25)
+
+
+def test_workload_generator_equals_oracle():
+    """The benchmark's own generator (alphazero-go_amd/workload) produces the
+    oracle's tensors and positions bit for bit."""
+    import workload as W
+    for tag in (1, 2):
+        w, ow = W.WORKLOADS[tag], O.WORKLOADS[tag]
+        t, ot = W.network_tensors(w.cfg), O.init_network(ow.cfg).tensors()
+        assert list(t) == list(ot)
+        for k in t:
+            assert np.array_equal(_bits(t[k]), _bits(ot[k])), k
+        a, la = W.positions(w, 16)
+        b, lb = O.workload_inputs(ow, 16)
+        assert np.array_equal(a, b) and np.array_equal(la, lb)
+        assert w.flops_per_position() == ow.flops_per_position()
