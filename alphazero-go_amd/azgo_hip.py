@@ -83,10 +83,11 @@ def load():
             "azh_synchronize": ([vp, C.c_int], C.c_int),
             "azh_fetch": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_time_passes": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
-            "azh_time_trunk_conv": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_time_tower_convs": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int)], C.c_int),
             "azh_time_round_trips": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    f32], C.c_int),
+            "azh_time_conv3x3": ([C.c_int] * 6 + [f32], C.c_int),
             "azh_probe_heads": ([vp, f32, C.c_int, f32, f32], C.c_int),
             "azh_probe_trunk": ([vp, f32, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_fill": ([f32, C.c_size_t, C.c_float, C.c_size_t], C.c_int),
@@ -242,10 +243,12 @@ class Runner:
         _check(self.lib.azh_time_passes(self.h, slot, B, iters, C.byref(ms)))
         return ms.value
 
-    def time_trunk_conv(self, slot, B, iters):
+    def time_tower_convs(self, slot, B, iters):
+        """(total ms, launches) of `iters` runs of the tower's convolutions."""
         ms = C.c_float()
-        _check(self.lib.azh_time_trunk_conv(self.h, slot, B, iters, C.byref(ms)))
-        return ms.value
+        n = C.c_int()
+        _check(self.lib.azh_time_tower_convs(self.h, slot, B, iters, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
 
     def time_round_trips(self, slot, B, iters):
         ms = C.c_float()
@@ -290,6 +293,13 @@ def probe_conv3x3(x, w, scale, shift, skip=None, relu=True, tiling=-1):
     _check(load().azh_probe_conv3x3(_f(x), _f(w), _f(_f32(scale)), _f(_f32(shift)),
                                     _f(sk) if sk is not None else None, int(relu), B, n, cin, cout, tiling, _f(y)))
     return y
+
+
+def time_conv3x3(B, n, cin, cout, tiling=-1, iters=10):
+    """Average ms of one 3x3 convolution launch (device-resident data)."""
+    ms = C.c_float()
+    _check(load().azh_time_conv3x3(B, n, cin, cout, tiling, iters, C.byref(ms)))
+    return ms.value / iters
 
 
 def probe_fill(data, n, value, tail=0):

@@ -46,12 +46,13 @@ __device__ inline float epilogue(float acc, float s, float h, const float* skip,
     return v;
 }
 
-template <int N, int COW, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restrict__ x, const f4* __restrict__ wp,
-                                                            const float* __restrict__ scale,
-                                                            const float* __restrict__ shift, const float* skip,
-                                                            float* y, int cin, int cout, int nq, int coTiles,
-                                                            int relu) {
+// MASKED: input channels past cin are read as zeros (the stem's 2H+2
+// planes); without it every chunk is whole (cin a multiple of 16).
+template <int N, int COW, int WAVES, bool MASKED>
+__device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
+                                            const float* __restrict__ scale, const float* __restrict__ shift,
+                                            const float* skip, float* y, int cin, int cout, int nq, int coTiles,
+                                            int relu) {
     using G = Geo<N>;
     constexpr int THREADS = WAVES * 64;
     constexpr int ITEMS = 4 * G::A;   // (channel group, point) pairs per chunk
@@ -65,7 +66,6 @@ __global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restr
     const int wg = blockIdx.x;
     const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
     const int b = logical / coTiles, ct = logical % coTiles;
-    const int coBlocks = (cout + 15) >> 4;
     const int cb0 = (ct * WAVES + wave) * COW;
     const int k = lane >> 4, n16 = lane & 15;
 
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restr
                 const int c0 = q * 16 + 4 * g;
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    if (c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+                    if (!MASKED || c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
             }
             stage[r] = v;
         }
@@ -121,25 +121,45 @@ __global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restr
     store(0);
     __syncthreads();
 
+    // The (tap, column group) steps of a chunk run as one unrolled stream:
+    // the B operand of step i + kRing is read from LDS while step i's MFMAs
+    // run, and each tap's A fragments are fetched from global memory one tap
+    // ahead, so neither read's latency stalls the matrix pipe. The sched
+    // group hints keep that interleave (a step's MFMAs, then the read kRing
+    // steps ahead).
+    constexpr int kRing = 4;
+    constexpr int STEPS = 9 * G::NPG;
+    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
+    auto loadA = [&](int q, int t, f4 (&a)[COW]) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
+    };
     for (int q = 0; q < nq; ++q) {
         if (q + 1 < nq) load(q + 1);
         const f4* buf = lds + (q & 1) * G::BUF;
+        f4 aCur[COW], aNext[COW];
+        loadA(q, 0, aCur);
+        f4 ring[kRing];
 #pragma unroll
-        for (int t = 0; t < 9; ++t) {
-            const int toff = (t / 3) * G::H + (t % 3);
-            f4 a[COW];
+        for (int i = 0; i < kRing; ++i) ring[i] = buf[rofs[i % G::NPG] + tapOffset(i / G::NPG)];
+        __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);   // the ring's first reads
 #pragma unroll
-            for (int c = 0; c < COW; ++c)
-                a[c] = (cb0 + c < coBlocks) ? wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane]
-                                            : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < STEPS; ++i) {
+            const int t = i / G::NPG, pg = i % G::NPG;
+            if (pg == 0 && t + 1 < 9) loadA(q, t + 1, aNext);
+            const f4 bv = ring[i % kRing];
+            if (i + kRing < STEPS)
+                ring[i % kRing] = buf[rofs[(i + kRing) % G::NPG] + tapOffset((i + kRing) / G::NPG)];
 #pragma unroll
-            for (int pg = 0; pg < G::NPG; ++pg) {
-                const f4 bv = buf[rofs[pg] + toff];
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int c = 0; c < COW; ++c)
+                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
+            if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
+            if (pg == G::NPG - 1 && t + 1 < 9) {
 #pragma unroll
-                    for (int c = 0; c < COW; ++c)
-                        acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][j], bv[j], acc[c][pg], 0, 0, 0);
+                for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
             }
         }
         if (q + 1 < nq) store((q + 1) & 1);
@@ -168,6 +188,29 @@ __global__ __launch_bounds__(WAVES * 64) void conv3x3Kernel(const float* __restr
     }
 }
 
+// The residual tower's convolutions (cin = filters, a multiple of 16) and
+// the stem's (cin = 2H+2 input planes) are separate kernels, so profiles
+// tell them apart.
+template <int N, int COW, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 ? 2 : 1, COW == 1 ? 2 : 1)))
+void conv3x3Tower(const float* __restrict__ x, const f4* __restrict__ wp,
+                                                           const float* __restrict__ scale,
+                                                           const float* __restrict__ shift, const float* skip,
+                                                           float* y, int cin, int cout, int nq, int coTiles,
+                                                           int relu) {
+    conv3x3Body<N, COW, WAVES, false>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, relu);
+}
+
+template <int N, int COW, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 ? 2 : 1, COW == 1 ? 2 : 1)))
+void conv3x3Stem(const float* __restrict__ x, const f4* __restrict__ wp,
+                                                          const float* __restrict__ scale,
+                                                          const float* __restrict__ shift, const float* skip,
+                                                          float* y, int cin, int cout, int nq, int coTiles,
+                                                          int relu) {
+    conv3x3Body<N, COW, WAVES, true>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, relu);
+}
+
 template <int N, int COW, int WAVES>
 hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
                        float* y, int B, int cin, int cout, bool relu, hipStream_t stream) {
@@ -175,9 +218,14 @@ hipError_t launchConvT(const float* x, const float* wp, const float* scale, cons
     const int coTiles = ceilDiv(cout, coTile);
     const int nq = ceilDiv(cin, kChunk);
     const dim3 grid(B * coTiles), block(WAVES * 64);
-    hipLaunchKernelGGL((conv3x3Kernel<N, COW, WAVES>), grid, block, 0, stream, x,
-                       reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
-                       relu ? 1 : 0);
+    if (cin % kChunk == 0)
+        hipLaunchKernelGGL((conv3x3Tower<N, COW, WAVES>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
+                           relu ? 1 : 0);
+    else
+        hipLaunchKernelGGL((conv3x3Stem<N, COW, WAVES>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
+                           relu ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -189,23 +237,24 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
     if (t.coPerWave == 1 && t.waves == 4) return launchConvT<N, 1, 4>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
     if (t.coPerWave == 1 && t.waves == 2) return launchConvT<N, 1, 2>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
     if (t.coPerWave == 1 && t.waves == 1) return launchConvT<N, 1, 1>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    if (t.coPerWave == 1 && t.waves == 8) return launchConvT<N, 1, 8>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
     return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------------ heads
 
+// The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
+// and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup:
+// act [B][3][A], planes 0-1 already the policy's flattened [2A] row
+// (feature c*A + p, src/network.cpp:278-285), plane 2 the value's [A] row.
 template <int N>
-__global__ __launch_bounds__(256) void headsKernel(const float* __restrict__ trunk, HeadWeights w,
-                                                   float* __restrict__ logits, float* __restrict__ values, int F,
-                                                   int V) {
-    constexpr int A = N * N, A1 = A + 1;
-    __shared__ float act[3 * A];   // policy planes 0 and 1 (the flattened [2A] row), then the value plane
-    __shared__ float hid[256];
-    const int b = blockIdx.x, tid = threadIdx.x;
+__global__ __launch_bounds__(256) void headConvKernel(const float* __restrict__ trunk, HeadWeights w,
+                                                      float* __restrict__ act, int F) {
+    constexpr int A = N * N;
+    const int b = blockIdx.x;
     const float* tb = trunk + (size_t)b * F * A;
-
-    // 1x1 convs F -> 3, BN, ReLU (src/network.cpp:274-277, 288-291).
-    for (int p = tid; p < A; p += 256) {
+    float* ab = act + (size_t)b * 3 * A;
+    for (int p = threadIdx.x; p < A; p += 256) {
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
         for (int c = 0; c < F; ++c) {
             const float xv = tb[(size_t)c * A + p];
@@ -213,33 +262,67 @@ __global__ __launch_bounds__(256) void headsKernel(const float* __restrict__ tru
             a1 = fmaf(w.convW[F + c], xv, a1);
             a2 = fmaf(w.convW[2 * F + c], xv, a2);
         }
-        act[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
-        act[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
-        act[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
+        ab[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
+        ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
+        ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
     }
-    __syncthreads();
+}
 
-    // Policy Linear: logits = flat . W^T, then + b (src/layers.cpp:169-176).
-    for (int a = tid; a < A1; a += 256) {
-        float s = 0.0f;
+// The heads' Linear layers for kFcBoards positions per workgroup, so each
+// weight is read once per group of positions. blockIdx.y < policy tiles:
+// 64 policy outputs, logits = flat . W^T + b (Linear::forward,
+// src/layers.cpp:169-176); the last y: the value head, fc1 (A -> V) + b,
+// ReLU, fc2 (V -> 1) + b, tanh (src/network.cpp:293-296). Every output is
+// one fmaf chain in input order, whatever the batch.
+constexpr int kFcBoards = 8;
+constexpr int kFcOutTile = 64;
+
+template <int N>
+__global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ act, HeadWeights w,
+                                                    float* __restrict__ logits, float* __restrict__ values, int B,
+                                                    int V) {
+    constexpr int A = N * N, A1 = A + 1, K = 2 * A;
+    __shared__ float xs[kFcBoards * 3 * A];
+    __shared__ float hid[kFcBoards * 256];
+    const int b0 = blockIdx.x * kFcBoards;
+    const int nb = min(kFcBoards, B - b0);
+    const int tid = threadIdx.x;
+    for (int i = tid; i < nb * 3 * A; i += 256) xs[i] = act[(size_t)b0 * 3 * A + i];
+    __syncthreads();
+    const int policyTiles = (A1 + kFcOutTile - 1) / kFcOutTile;
+    if ((int)blockIdx.y < policyTiles) {
+        const int a = blockIdx.y * kFcOutTile + (tid & (kFcOutTile - 1));
+        const int g = tid >> 6;   // boards g and g + 4
+        if (a >= A1) return;
+        float s0 = 0.0f, s1 = 0.0f;
+        const float* x0 = xs + g * 3 * A;
+        const float* x1 = xs + (g + 4) * 3 * A;
         const float* wc = w.policyWT + a;
-        for (int i = 0; i < 2 * A; ++i) s = fmaf(act[i], wc[(size_t)i * A1], s);
-        logits[(size_t)b * A1 + a] = __fadd_rn(s, w.policyB[a]);
+        for (int i = 0; i < K; ++i) {
+            const float wv = wc[(size_t)i * A1];
+            s0 = fmaf(x0[i], wv, s0);
+            s1 = fmaf(x1[i], wv, s1);
+        }
+        if (g < nb) logits[(size_t)(b0 + g) * A1 + a] = __fadd_rn(s0, w.policyB[a]);
+        if (g + 4 < nb) logits[(size_t)(b0 + g + 4) * A1 + a] = __fadd_rn(s1, w.policyB[a]);
+        return;
     }
-    // Value Linear A -> V, + b, ReLU.
-    for (int v = tid; v < V; v += 256) {
-        float s = 0.0f;
+    // Value head: thread (v, board group) over V hidden units.
+    for (int idx = tid; idx < kFcBoards * V; idx += 256) {
+        const int bb = idx / V, v = idx - bb * V;
+        if (bb >= nb) continue;
+        const float* xv = xs + bb * 3 * A + 2 * A;
         const float* wc = w.fc1WT + v;
-        for (int p = 0; p < A; ++p) s = fmaf(act[2 * A + p], wc[(size_t)p * V], s);
+        float s = 0.0f;
+        for (int p = 0; p < A; ++p) s = fmaf(xv[p], wc[(size_t)p * V], s);
         s = __fadd_rn(s, w.fc1B[v]);
-        hid[v] = s > 0.0f ? s : 0.0f;
+        hid[bb * 256 + v] = s > 0.0f ? s : 0.0f;
     }
     __syncthreads();
-    // Value Linear V -> 1, + b, tanh.
-    if (tid == 0) {
+    if (tid < nb) {
         float s = 0.0f;
-        for (int v = 0; v < V; ++v) s = fmaf(hid[v], w.fc2W[v], s);
-        values[b] = tanhf(__fadd_rn(s, w.fc2B[0]));
+        for (int v = 0; v < V; ++v) s = fmaf(hid[tid * 256 + v], w.fc2W[v], s);
+        values[b0 + tid] = tanhf(__fadd_rn(s, w.fc2B[0]));
     }
 }
 
@@ -290,11 +373,11 @@ __global__ void fillKernel(float* data, size_t n, float value) {
 // ------------------------------------------------------------------ host side
 
 size_t packedConv3x3Floats(int cin, int cout) {
-    return (size_t)ceilDiv(cout, kCoBlock) * ceilDiv(cin, kChunk) * 9 * 64 * 4;
+    return (size_t)packedCoBlocks(cout) * ceilDiv(cin, kChunk) * 9 * 64 * 4;
 }
 
 std::vector<float> packConv3x3(const float* w, int cin, int cout) {
-    const int coBlocks = ceilDiv(cout, kCoBlock), nq = ceilDiv(cin, kChunk);
+    const int coBlocks = packedCoBlocks(cout), nq = ceilDiv(cin, kChunk);
     std::vector<float> out(packedConv3x3Floats(cin, cout), 0.0f);
     for (int cb = 0; cb < coBlocks; ++cb)
         for (int q = 0; q < nq; ++q)
@@ -312,12 +395,14 @@ std::vector<float> packConv3x3(const float* w, int cin, int cout) {
 bool conv3x3Supported(int n) { return n == 5 || n == 9 || n == 13 || n == 19; }
 
 ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
+    (void)B;
     (void)boardSize;
-    // Enough workgroups to cover the 256 CUs where the batch is small;
-    // otherwise the widest tile (fewest re-reads of the board in LDS).
+    // 4 waves of 16 output channels each: 64 per workgroup, so the headline
+    // layer (256 boards x 128 channels) is 512 workgroups, two resident per
+    // CU (226 registers per lane, 56 KB of LDS each), one hiding the other's
+    // staging, barriers and epilogue. Measured fastest of the shapes at
+    // every batch from 1 to 512 on 19x19 and 9x9 boards.
     const int coBlocks = ceilDiv(cout, kCoBlock);
-    if (coBlocks >= 8 && B >= 128) return {2, 4};
-    if (coBlocks >= 4 && B >= 64) return {2, 2};
     if (coBlocks >= 4) return {1, 4};
     if (coBlocks >= 2) return {1, 2};
     return {1, 1};
@@ -336,16 +421,23 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
     }
 }
 
-hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* logits, float* values, int B, int n, int F,
-                       int V, hipStream_t stream) {
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values, int B,
+                       int n, int F, int V, hipStream_t stream) {
     if (B < 1) return hipSuccess;
     if (V > 256) return hipErrorInvalidValue;
-    const dim3 grid(B), block(256);
+    const int A1 = n * n + 1;
+    const dim3 grid1(B), grid2(ceilDiv(B, kFcBoards), ceilDiv(A1, kFcOutTile) + 1), block(256);
     switch (n) {
-    case 5: hipLaunchKernelGGL(headsKernel<5>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
-    case 9: hipLaunchKernelGGL(headsKernel<9>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
-    case 13: hipLaunchKernelGGL(headsKernel<13>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
-    case 19: hipLaunchKernelGGL(headsKernel<19>, grid, block, 0, stream, trunk, w, logits, values, F, V); break;
+#define AZH_HEADS(NN)                                                                                         \
+    case NN:                                                                                                  \
+        hipLaunchKernelGGL(headConvKernel<NN>, grid1, block, 0, stream, trunk, w, act, F);                   \
+        hipLaunchKernelGGL(headFcKernel<NN>, grid2, block, 0, stream, act, w, logits, values, B, V);         \
+        break;
+        AZH_HEADS(5)
+        AZH_HEADS(9)
+        AZH_HEADS(13)
+        AZH_HEADS(19)
+#undef AZH_HEADS
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -21,11 +21,15 @@ constexpr int kCoBlock = 16;
 
 inline int ceilDiv(int a, int b) { return (a + b - 1) / b; }
 
+// Output-channel blocks of packed weights: ceil(cout/16) rounded up to whole
+// 128-channel workgroup tiles, so no workgroup shape reads past them.
+inline int packedCoBlocks(int cout) { return ceilDiv(ceilDiv(cout, kCoBlock), 8) * 8; }
+
 // A 3x3 convolution's weights w [cout][cin][3][3] (Conv2d::w,
 // include/azgo/layers.hpp:32, row (c*3 + dy)*3 + dx) packed as the MFMA A
 // fragments the kernel loads: [co block][chunk q][tap t][lane 0..63][j 0..3],
 // value w[cb*16 + (lane & 15)][q*16 + 4*(lane >> 4) + j][t], zero where the
-// output or input channel is padding. coBlocks = ceil(cout/16),
+// output or input channel is padding. co blocks = packedCoBlocks(cout),
 // chunks = ceil(cin/16).
 std::vector<float> packConv3x3(const float* w, int cin, int cout);
 size_t packedConv3x3Floats(int cin, int cout);
@@ -37,7 +41,7 @@ size_t packedConv3x3Floats(int cin, int cout);
 // so results are bitwise independent of the cut and of the batch.
 struct ConvTiling {
     int coPerWave;   // MFMA co blocks per wave: 1 or 2
-    int waves;       // waves per workgroup: 1, 2 or 4
+    int waves;       // waves per workgroup: 1, 2, 4 or 8 (at most 128 channels)
     int coTile() const { return 16 * coPerWave * waves; }
 };
 ConvTiling chooseConvTiling(int cout, int B, int boardSize);
@@ -52,10 +56,10 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
                          hipStream_t stream);
 bool conv3x3Supported(int boardSize);
 
-// The policy and value heads of one position per workgroup, fused:
-// 1x1 convs F -> 2 and F -> 1 with BN and ReLU, the policy Linear
-// (2A -> A+1) and the value Linears (A -> V, ReLU, V -> 1) and tanh
-// (src/network.cpp:274-296).
+// The policy and value heads (src/network.cpp:274-296), two kernels: the
+// 1x1 convs F -> 2 and F -> 1 with BN and ReLU, one position per workgroup,
+// into act [B][3][n*n]; then the policy Linear (2A -> A+1) and the value
+// Linears (A -> V, ReLU, V -> 1) and tanh, 8 positions per workgroup.
 struct HeadWeights {
     const float* convW;      // [3][F]: policy rows 0-1, value row 2
     const float* scale;      // [3] folded BN scale
@@ -67,8 +71,8 @@ struct HeadWeights {
     const float* fc2W;       // [V]
     const float* fc2B;       // [1]
 };
-hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* logits, float* values, int B, int n, int F,
-                       int V, hipStream_t stream);
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values, int B,
+                       int n, int F, int V, hipStream_t stream);
 
 // priors[b][a] = exp(l - max) / sum over legal a of the same, 0 where
 // illegal (Mcts::expand's softmax, src/mcts.cpp:170-183). One wavefront per

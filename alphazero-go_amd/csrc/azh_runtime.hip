@@ -76,6 +76,9 @@ constexpr size_t kMemoryMargin = size_t(512) << 20;
 // the tree search needs.
 constexpr int kPollFirstUs = 50, kPollLastUs = 200;
 constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
+// The workgroup shapes a probe may force (co blocks per wave, waves).
+const azh::ConvTiling kTilings[] = {{2, 4}, {2, 2}, {1, 4}, {1, 2}, {1, 1}, {1, 8}};
+constexpr int kTilingCount = sizeof kTilings / sizeof kTilings[0];
 
 // ---------------------------------------------------------------- context
 
@@ -103,6 +106,11 @@ struct Context {
             return;
         }
         name = p.name;
+        if (name.empty()) {
+            char buf[256] = {};
+            if (hipDeviceGetName(buf, sizeof buf, dev) == hipSuccess) name = buf;
+        }
+        if (name.empty()) name = "AMD GPU";
         arch = p.gcnArchName;
         const std::string base = arch.substr(0, arch.find(':'));
         (void)hipRuntimeGetVersion(&runtime);
@@ -340,7 +348,8 @@ void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*
 
 size_t slotFloats(const Shape& s, int maxBatch) {
     const size_t B = maxBatch;
-    return alignFloats(B * s.P * s.A) + 2 * alignFloats(B * s.F * s.A) + alignFloats(B * s.A1) + alignFloats(B);
+    return alignFloats(B * s.P * s.A) + 2 * alignFloats(B * s.F * s.A) + alignFloats(B * 3 * s.A) +
+           alignFloats(B * s.A1) + alignFloats(B);
 }
 
 size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
@@ -351,7 +360,7 @@ struct Slot {
     hipStream_t stream = nullptr;
     hipEvent_t event = nullptr;
     float* dev = nullptr;
-    float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dLogits = nullptr, *dValues = nullptr;
+    float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dAct = nullptr, *dLogits = nullptr, *dValues = nullptr;
     float *hIn = nullptr, *hLogits = nullptr, *hValues = nullptr;
     std::map<int, hipGraphExec_t> graphs;
     bool busy = false;
@@ -370,6 +379,7 @@ struct Slot {
         dIn = take(B * s.P * s.A);
         dX = take(B * s.F * s.A);
         dMid = take(B * s.F * s.A);
+        dAct = take(B * 3 * s.A);
         dLogits = take(B * s.A1);
         dValues = take(B);
         check(hipHostMalloc((void**)&hIn, B * s.P * s.A * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
@@ -488,7 +498,8 @@ struct azh_runner {
                   "conv3x3 (conv2)");
         }
         if (heads)
-            check(azh::launchHeads(s.dX, weights.heads, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, stream), "heads");
+            check(azh::launchHeads(s.dX, weights.heads, s.dAct, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, stream),
+                  "heads");
     }
 
     // The device-resident pass: one captured graph per batch size, replayed.
@@ -804,20 +815,29 @@ int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms) {
     });
 }
 
-int azh_time_trunk_conv(azh_runner* r, int slot, int B, int iters, float* ms) {
+int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches) {
     return guarded([&] {
-        if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        if (!r || !ms || !launches || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
         r->checkBatch(B);
         Slot& s = r->idleSlot(slot);
         const Shape& sh = r->shape;
         const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
-        const ConvW& w = r->weights.conv1[0];
+        // The tower as the pass runs it: every block's two convolutions in
+        // order, each reading the previous one's output.
         *ms = timeOnStream(s.stream, iters, [&] {
-            check(azh::launchConv3x3(s.dX, w.w, w.scale, w.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
-                                     s.stream),
-                  "conv3x3");
+            for (int i = 0; i < sh.blocks; ++i) {
+                const ConvW& a = r->weights.conv1[i];
+                const ConvW& b = r->weights.conv2[i];
+                check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
+                                         s.stream),
+                      "conv3x3");
+                check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, t,
+                                         s.stream),
+                      "conv3x3");
+            }
         });
+        *launches = iters * 2 * sh.blocks;
     });
 }
 
@@ -843,9 +863,8 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
         if (!x || !w || !scale || !shift || !y || B < 1 || cin < 1 || cout < 1)
             throw Error(AZH_ERR_ARGUMENT, "hip: bad conv probe arguments");
         if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
-        static const azh::ConvTiling table[] = {{2, 4}, {2, 2}, {1, 4}, {1, 2}, {1, 1}};
-        if (tiling < -1 || tiling > 4) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index outside [-1, 4]");
-        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : table[tiling];
+        if (tiling < -1 || tiling >= kTilingCount) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index out of range");
+        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : kTilings[tiling];
         requireContext();
         const size_t A = (size_t)n * n;
         const std::vector<float> packed = azh::packConv3x3(w, cin, cout);
@@ -879,6 +898,51 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
     });
 }
 
+int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, float* ms) {
+    return guarded([&] {
+        if (!ms || B < 1 || cin < 1 || cout < 1 || iters < 1)
+            throw Error(AZH_ERR_ARGUMENT, "hip: bad conv timing arguments");
+        if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
+        if (tiling < -1 || tiling >= kTilingCount) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index out of range");
+        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : kTilings[tiling];
+        requireContext();
+        const size_t A = (size_t)n * n;
+        std::vector<float> w((size_t)cout * cin * 9);
+        uint32_t st = 12345;
+        for (float& v : w) {
+            st = st * 1664525u + 1013904223u;
+            v = ((st >> 8) * (1.0f / 16777216.0f) - 0.5f) * 0.05f;
+        }
+        const std::vector<float> packed = azh::packConv3x3(w.data(), cin, cout);
+        std::vector<float*> bufs;
+        struct Free {
+            std::vector<float*>& b;
+            ~Free() {
+                for (float* p : b) (void)hipFree(p);
+            }
+        } guard{bufs};
+        auto dev = [&](size_t floats) {
+            float* p = nullptr;
+            check(hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float)), "hipMalloc");
+            bufs.push_back(p);
+            return p;
+        };
+        float* dx = dev(B * cin * A);
+        float* dw = dev(packed.size());
+        float* ds = dev(cout);
+        float* dh = dev(cout);
+        float* dy = dev(B * cout * A);
+        check(azh::launchFill(dx, B * cin * A, 0.5f, nullptr), "fill");
+        check(azh::launchFill(ds, cout, 1.0f, nullptr), "fill");
+        check(azh::launchFill(dh, cout, 0.0f, nullptr), "fill");
+        check(hipMemcpy(dw, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchConv3x3(dx, dw, ds, dh, nullptr, dy, B, n, cin, cout, true, t, nullptr), "conv3x3");
+        *ms = timeOnStream(nullptr, iters, [&] {
+            check(azh::launchConv3x3(dx, dw, ds, dh, dy, dy, B, n, cin, cout, true, t, nullptr), "conv3x3");
+        });
+    });
+}
+
 int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values) {
     return guarded([&] {
         if (!r || !trunk || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: bad heads probe arguments");
@@ -887,7 +951,8 @@ int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, flo
         const Shape& sh = r->shape;
         check(hipMemcpyAsync(s.dX, trunk, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
-        check(azh::launchHeads(s.dX, r->weights.heads, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, s.stream), "heads");
+        check(azh::launchHeads(s.dX, r->weights.heads, s.dAct, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, s.stream),
+              "heads");
         check(hipMemcpyAsync(logits, s.dLogits, (size_t)B * sh.A1 * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");
         check(hipMemcpyAsync(values, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),

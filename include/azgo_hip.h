@@ -162,9 +162,11 @@ int azh_fetch(azh_runner* r, int slot, int B);
 /* HIP events on the slot's stream around `iters` device-resident passes:
  * total milliseconds. */
 int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms);
-/* HIP events on the slot's stream around `iters` launches of the first
- * residual block's first convolution alone (the dominant kernel): total ms. */
-int azh_time_trunk_conv(azh_runner* r, int slot, int B, int iters, float* ms);
+/* HIP events on the slot's stream around `iters` runs of the residual
+ * tower's convolutions as the pass runs them (every block's two, in order,
+ * on the slot's staged data): total ms and the number of launches timed,
+ * for the dominant kernel's average launch time. */
+int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches);
 /* Events around `iters` synchronous round trips: pinned H2D, pass, D2H. */
 int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
 
@@ -173,9 +175,15 @@ int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
 /* The pass's 3x3 convolution kernel alone (cuda_probe::convBnRelu,
  * include/azgo/cuda.hpp:123-126): x [B][cin][n*n], w [cout][cin*9],
  * y [B][cout][n*n] = relu?(scale*conv + shift (+ skip)). skip may be NULL.
- * tiling: -1 the pass's rule, else an index 0..4 forcing a workgroup shape. */
+ * tiling: -1 the pass's rule, else an index 0..5 forcing a workgroup shape
+ * (co blocks per wave x waves: 2x4, 2x2, 1x4, 1x2, 1x1, 1x8). */
 int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const float* shift, const float* skip,
                       int relu, int B, int n, int cin, int cout, int tiling, float* y);
+
+/* HIP events around `iters` launches of the 3x3 convolution kernel alone on
+ * device-resident synthetic data (x [B][cin][n*n] -> y), tiling as above:
+ * total ms. For tuning the workgroup shape. */
+int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, float* ms);
 
 /* The heads kernel alone on the runner's weights: trunk [B][F][n*n] ->
  * logits, values. */

@@ -43,15 +43,15 @@ def test_built_and_describe_without_gpu_is_an_answer():
 
 
 def test_memory_need_formula():
-    """Per slot: input, two trunk buffers, logits, values (256-byte aligned);
-    plus the packed weights once."""
+    """Per slot: input, two trunk buffers, the heads' 3 planes, logits,
+    values (256-byte aligned); plus the packed weights once."""
     cfg = to_hip_cfg(azgo_hip, O.WORKLOADS[3].cfg)
     one = azgo_hip.memory_need(cfg, 256, 1)
     two = azgo_hip.memory_need(cfg, 256, 2)
     slot = two - one
     al = lambda f: (f + 63) // 64 * 64   # noqa: E731
     B, P, A, F = 256, 18, 361, 128
-    assert slot == 4 * (al(B * P * A) + 2 * al(B * F * A) + al(B * (A + 1)) + al(B))
+    assert slot == 4 * (al(B * P * A) + 2 * al(B * F * A) + al(B * 3 * A) + al(B * (A + 1)) + al(B))
     weights = one - slot
     assert 13e6 < weights < 16e6   # ~3.27 M parameters, packed with channel padding
 
