@@ -192,7 +192,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
 // the stem's (cin = 2H+2 input planes) are separate kernels, so profiles
 // tell them apart.
 template <int N, int COW, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 ? 2 : 1, COW == 1 ? 2 : 1)))
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 && WAVES >= 4 ? 2 : 1, COW == 1 && WAVES >= 4 ? 2 : 1)))
 void conv3x3Tower(const float* __restrict__ x, const f4* __restrict__ wp,
                                                            const float* __restrict__ scale,
                                                            const float* __restrict__ shift, const float* skip,
@@ -202,7 +202,7 @@ void conv3x3Tower(const float* __restrict__ x, const f4* __restrict__ wp,
 }
 
 template <int N, int COW, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 ? 2 : 1, COW == 1 ? 2 : 1)))
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 && WAVES >= 4 ? 2 : 1, COW == 1 && WAVES >= 4 ? 2 : 1)))
 void conv3x3Stem(const float* __restrict__ x, const f4* __restrict__ wp,
                                                           const float* __restrict__ scale,
                                                           const float* __restrict__ shift, const float* skip,
@@ -244,84 +244,119 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 // ------------------------------------------------------------------ heads
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
-// and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup:
-// act [B][3][A], planes 0-1 already the policy's flattened [2A] row
-// (feature c*A + p, src/network.cpp:278-285), plane 2 the value's [A] row.
+// and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
+// one point per thread, loads hoisted 16 channels ahead of their FMAs:
+// act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
+// src/network.cpp:278-285), plane 2 the value's [A] row.
 template <int N>
-__global__ __launch_bounds__(256) void headConvKernel(const float* __restrict__ trunk, HeadWeights w,
-                                                      float* __restrict__ act, int F) {
+__global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const float* __restrict__ trunk,
+                                                                          HeadWeights w, float* __restrict__ act,
+                                                                          int F) {
     constexpr int A = N * N;
-    const int b = blockIdx.x;
-    const float* tb = trunk + (size_t)b * F * A;
-    float* ab = act + (size_t)b * 3 * A;
-    for (int p = threadIdx.x; p < A; p += 256) {
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
-        for (int c = 0; c < F; ++c) {
-            const float xv = tb[(size_t)c * A + p];
-            a0 = fmaf(w.convW[c], xv, a0);
-            a1 = fmaf(w.convW[F + c], xv, a1);
-            a2 = fmaf(w.convW[2 * F + c], xv, a2);
+    const int b = blockIdx.x, p = threadIdx.x;
+    if (p >= A) return;
+    const float* tb = trunk + (size_t)b * F * A + p;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
+    for (int c0 = 0; c0 < F; c0 += 16) {
+        float xv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) xv[u] = c0 + u < F ? tb[(size_t)(c0 + u) * A] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            if (c0 + u < F) {
+                a0 = fmaf(w.convW[c0 + u], xv[u], a0);
+                a1 = fmaf(w.convW[F + c0 + u], xv[u], a1);
+                a2 = fmaf(w.convW[2 * F + c0 + u], xv[u], a2);
+            }
         }
-        ab[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
-        ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
-        ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
     }
+    float* ab = act + (size_t)b * 3 * A;
+    ab[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
+    ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
+    ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
 }
 
-// The heads' Linear layers for kFcBoards positions per workgroup, so each
-// weight is read once per group of positions. blockIdx.y < policy tiles:
-// 64 policy outputs, logits = flat . W^T + b (Linear::forward,
+// The heads' Linear layers as MFMA GEMMs over 16 positions per workgroup
+// (one 16 x 16 output block per wave, v_mfma_f32_16x16x4_f32). blockIdx.y <
+// policy tiles: 64 policy outputs, logits = flat . W^T + b (Linear::forward,
 // src/layers.cpp:169-176); the last y: the value head, fc1 (A -> V) + b,
-// ReLU, fc2 (V -> 1) + b, tanh (src/network.cpp:293-296). Every output is
-// one fmaf chain in input order, whatever the batch.
-constexpr int kFcBoards = 8;
+// ReLU, fc2 (V -> 1) + b, tanh (src/network.cpp:293-296). The positions'
+// rows are staged in LDS, zero past the batch and past K; the weights come
+// pre-transposed and zero-padded to whole 16 x 16 blocks (HeadWeights).
+// Each output is a dot product over its own row only, in a fixed K order.
+constexpr int kFcBoards = 16;
 constexpr int kFcOutTile = 64;
+
+__host__ __device__ constexpr int headPad16(int x) { return (x + 15) / 16 * 16; }
 
 template <int N>
 __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ act, HeadWeights w,
                                                     float* __restrict__ logits, float* __restrict__ values, int B,
                                                     int V) {
-    constexpr int A = N * N, A1 = A + 1, K = 2 * A;
-    __shared__ float xs[kFcBoards * 3 * A];
+    constexpr int A = N * N, A1 = A + 1;
+    constexpr int KP = headPad16(2 * A);          // policy K, padded
+    constexpr int KV = headPad16(A);              // value K, padded
+    constexpr int NP = headPad16(A1);             // policy outputs, padded
+    constexpr int RS = KP + 4;                    // LDS row stride (floats)
+    __shared__ f4 xs4[kFcBoards * RS / 4];
     __shared__ float hid[kFcBoards * 256];
+    float* xs = reinterpret_cast<float*>(xs4);
     const int b0 = blockIdx.x * kFcBoards;
     const int nb = min(kFcBoards, B - b0);
-    const int tid = threadIdx.x;
-    for (int i = tid; i < nb * 3 * A; i += 256) xs[i] = act[(size_t)b0 * 3 * A + i];
-    __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int policyTiles = (A1 + kFcOutTile - 1) / kFcOutTile;
-    if ((int)blockIdx.y < policyTiles) {
-        const int a = blockIdx.y * kFcOutTile + (tid & (kFcOutTile - 1));
-        const int g = tid >> 6;   // boards g and g + 4
-        if (a >= A1) return;
-        float s0 = 0.0f, s1 = 0.0f;
-        const float* x0 = xs + g * 3 * A;
-        const float* x1 = xs + (g + 4) * 3 * A;
-        const float* wc = w.policyWT + a;
-        for (int i = 0; i < K; ++i) {
-            const float wv = wc[(size_t)i * A1];
-            s0 = fmaf(x0[i], wv, s0);
-            s1 = fmaf(x1[i], wv, s1);
+    const bool policy = (int)blockIdx.y < policyTiles;
+    const int K = policy ? 2 * A : A, KPad = policy ? KP : KV;
+    const int src = policy ? 0 : 2 * A;
+    for (int i = tid; i < kFcBoards * KPad; i += 256) {
+        const int bb = i / KPad, k = i - bb * KPad;
+        xs[bb * RS + k] = (bb < nb && k < K) ? act[(size_t)(b0 + bb) * 3 * A + src + k] : 0.0f;
+    }
+    __syncthreads();
+
+    const int m = lane & 15, kk = lane >> 4;
+    // One 16 x 16 block: positions 0..15 x columns n0..n0+15 of W^T [KPad][ld].
+    auto block = [&](int n0, int ld, const float* wt) {
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k0 = 0; k0 < KPad; k0 += 16) {
+            const f4 av = xs4[(m * RS + k0) / 4 + kk];
+            const float* wr = wt + (size_t)(k0 + 4 * kk) * ld + n0 + m;
+            float bv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = wr[(size_t)j * ld];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
         }
-        if (g < nb) logits[(size_t)(b0 + g) * A1 + a] = __fadd_rn(s0, w.policyB[a]);
-        if (g + 4 < nb) logits[(size_t)(b0 + g + 4) * A1 + a] = __fadd_rn(s1, w.policyB[a]);
+        return acc;   // lane holds (position 4*kk + r, column n0 + m)
+    };
+    if (policy) {
+        const int n0 = blockIdx.y * kFcOutTile + wave * 16;
+        if (n0 >= NP) return;
+        const f4 acc = block(n0, NP, w.policyWT);
+        const int a = n0 + m;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int bb = 4 * kk + r;
+            if (bb < nb && a < A1) logits[(size_t)(b0 + bb) * A1 + a] = __fadd_rn(acc[r], w.policyB[a]);
+        }
         return;
     }
-    // Value head: thread (v, board group) over V hidden units.
-    for (int idx = tid; idx < kFcBoards * V; idx += 256) {
-        const int bb = idx / V, v = idx - bb * V;
-        if (bb >= nb) continue;
-        const float* xv = xs + bb * 3 * A + 2 * A;
-        const float* wc = w.fc1WT + v;
-        float s = 0.0f;
-        for (int p = 0; p < A; ++p) s = fmaf(xv[p], wc[(size_t)p * V], s);
-        s = __fadd_rn(s, w.fc1B[v]);
-        hid[bb * 256 + v] = s > 0.0f ? s : 0.0f;
+    const int VP = headPad16(V);
+    for (int n0 = wave * 16; n0 < VP; n0 += 64) {
+        const f4 acc = block(n0, VP, w.fc1WT);
+        const int v = n0 + m;
+        if (v < V) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float h = __fadd_rn(acc[r], w.fc1B[v]);
+                hid[(4 * kk + r) * 256 + v] = h > 0.0f ? h : 0.0f;
+            }
+        }
     }
     __syncthreads();
     if (tid < nb) {
         float s = 0.0f;
-        for (int v = 0; v < V; ++v) s = fmaf(hid[tid * 256 + v], w.fc2W[v], s);
+        for (int u = 0; u < V; ++u) s = fmaf(hid[tid * 256 + u], w.fc2W[u], s);
         values[b0 + tid] = tanhf(__fadd_rn(s, w.fc2B[0]));
     }
 }
@@ -426,12 +461,13 @@ hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, flo
     if (B < 1) return hipSuccess;
     if (V > 256) return hipErrorInvalidValue;
     const int A1 = n * n + 1;
-    const dim3 grid1(B), grid2(ceilDiv(B, kFcBoards), ceilDiv(A1, kFcOutTile) + 1), block(256);
+    const dim3 grid1(B), grid2(ceilDiv(B, kFcBoards), ceilDiv(A1, kFcOutTile) + 1);
+    const dim3 block1(ceilDiv(n * n, 64) * 64), block2(256);
     switch (n) {
 #define AZH_HEADS(NN)                                                                                         \
     case NN:                                                                                                  \
-        hipLaunchKernelGGL(headConvKernel<NN>, grid1, block, 0, stream, trunk, w, act, F);                   \
-        hipLaunchKernelGGL(headFcKernel<NN>, grid2, block, 0, stream, act, w, logits, values, B, V);         \
+        hipLaunchKernelGGL(headConvKernel<NN>, grid1, block1, 0, stream, trunk, w, act, F);                  \
+        hipLaunchKernelGGL(headFcKernel<NN>, grid2, block2, 0, stream, act, w, logits, values, B, V);        \
         break;
         AZH_HEADS(5)
         AZH_HEADS(9)
@@ -442,6 +478,9 @@ hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, flo
     }
     return hipGetLastError();
 }
+
+size_t headPolicyWTFloats(int n) { return (size_t)headPad16(2 * n * n) * headPad16(n * n + 1); }
+size_t headFc1WTFloats(int n, int V) { return (size_t)headPad16(n * n) * headPad16(V); }
 
 hipError_t launchSoftmaxLegal(const float* logits, const uint8_t* legal, float* priors, int B, int actions,
                               hipStream_t stream) {

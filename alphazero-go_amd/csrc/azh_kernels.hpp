@@ -59,18 +59,21 @@ bool conv3x3Supported(int boardSize);
 // The policy and value heads (src/network.cpp:274-296), two kernels: the
 // 1x1 convs F -> 2 and F -> 1 with BN and ReLU, one position per workgroup,
 // into act [B][3][n*n]; then the policy Linear (2A -> A+1) and the value
-// Linears (A -> V, ReLU, V -> 1) and tanh, 8 positions per workgroup.
+// Linears (A -> V, ReLU, V -> 1) and tanh as MFMA GEMMs, 16 positions per
+// workgroup. V at most 256.
 struct HeadWeights {
     const float* convW;      // [3][F]: policy rows 0-1, value row 2
     const float* scale;      // [3] folded BN scale
     const float* shift;      // [3] folded BN shift
-    const float* policyWT;   // [2A][A+1]: policy.fc.w transposed
+    const float* policyWT;   // [pad16(2A)][pad16(A+1)]: policy.fc.w transposed, zero-padded
     const float* policyB;    // [A+1]
-    const float* fc1WT;      // [A][V]: value.fc1.w transposed
+    const float* fc1WT;      // [pad16(A)][pad16(V)]: value.fc1.w transposed, zero-padded
     const float* fc1B;       // [V]
     const float* fc2W;       // [V]
     const float* fc2B;       // [1]
 };
+size_t headPolicyWTFloats(int n);
+size_t headFc1WTFloats(int n, int V);
 hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values, int B,
                        int n, int F, int V, hipStream_t stream);
 

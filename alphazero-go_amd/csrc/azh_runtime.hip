@@ -236,8 +236,8 @@ size_t weightFloats(const azh_netcfg& c) {
     f += alignFloats(azh::packedConv3x3Floats(s.P, s.F)) + 2 * alignFloats(s.F);
     f += (size_t)s.blocks * 2 * (alignFloats(azh::packedConv3x3Floats(s.F, s.F)) + 2 * alignFloats(s.F));
     f += alignFloats(3 * s.F) + 2 * alignFloats(3);
-    f += alignFloats((size_t)2 * s.A * s.A1) + alignFloats(s.A1);
-    f += alignFloats((size_t)s.A * s.V) + alignFloats(s.V) + alignFloats(s.V) + alignFloats(1);
+    f += alignFloats(azh::headPolicyWTFloats(s.n)) + alignFloats(s.A1);
+    f += alignFloats(azh::headFc1WTFloats(s.n, s.V)) + alignFloats(s.V) + alignFloats(s.V) + alignFloats(1);
     return f;
 }
 
@@ -317,15 +317,19 @@ void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*
            &host[hScale], &host[hShift]);
     foldBn(T("value.bn.gamma"), T("value.bn.beta"), T("value.bn.runMean"), T("value.bn.runVar"), 1,
            &host[hScale + 2], &host[hShift + 2]);
-    const size_t pW = take((size_t)2 * s.A * s.A1), pB = take(s.A1);
+    // The head Linears transposed ([in][out]) and zero-padded to whole 16 x 16
+    // MFMA blocks.
+    const size_t np = azh::headPolicyWTFloats(s.n) / (size_t)((2 * s.A + 15) / 16 * 16);
+    const size_t pW = take(azh::headPolicyWTFloats(s.n)), pB = take(s.A1);
     const float* pw = T("policy.fc.w");   // [A+1][2A]
     for (int a = 0; a < s.A1; ++a)
-        for (int i = 0; i < 2 * s.A; ++i) host[pW + (size_t)i * s.A1 + a] = pw[(size_t)a * 2 * s.A + i];
+        for (int i = 0; i < 2 * s.A; ++i) host[pW + (size_t)i * np + a] = pw[(size_t)a * 2 * s.A + i];
     std::copy(T("policy.fc.b"), T("policy.fc.b") + s.A1, host.begin() + pB);
-    const size_t f1W = take((size_t)s.A * s.V), f1B = take(s.V), f2W = take(s.V), f2B = take(1);
+    const size_t f1W = take(azh::headFc1WTFloats(s.n, s.V)), f1B = take(s.V), f2W = take(s.V), f2B = take(1);
     const float* w1 = T("value.fc1.w");   // [V][A]
+    const size_t vp = (size_t)(s.V + 15) / 16 * 16;
     for (int v = 0; v < s.V; ++v)
-        for (int p = 0; p < s.A; ++p) host[f1W + (size_t)p * s.V + v] = w1[(size_t)v * s.A + p];
+        for (int p = 0; p < s.A; ++p) host[f1W + (size_t)p * vp + v] = w1[(size_t)v * s.A + p];
     std::copy(T("value.fc1.b"), T("value.fc1.b") + s.V, host.begin() + f1B);
     std::copy(T("value.fc2.w"), T("value.fc2.w") + s.V, host.begin() + f2W);
     host[f2B] = T("value.fc2.b")[0];
