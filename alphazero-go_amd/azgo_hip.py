@@ -67,6 +67,7 @@ def load():
             "azh_last_error": ([], C.c_char_p),
             "azh_memory_need": ([P(NetCfg), C.c_int, C.c_int, P(C.c_size_t)], C.c_int),
             "azh_check_memory": ([P(NetCfg), C.c_int, C.c_int, C.c_int], C.c_int),
+            "azh_check_memory_bytes": ([C.c_double, C.c_int, C.c_int], C.c_int),
             "azh_create": ([P(NetCfg), P(Tensor), C.c_int, C.c_int, C.c_int, P(vp)], C.c_int),
             "azh_destroy": ([vp], None),
             "azh_slots": ([vp], C.c_int),

@@ -652,6 +652,15 @@ int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_p
     });
 }
 
+int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs) {
+    return guarded([&] {
+        if (!(need_bytes >= 0) || max_batch < 1 || hubs < 1)
+            throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: bad arguments");
+        requireContext();
+        checkFits(need_bytes, max_batch, hubs);
+    });
+}
+
 int azh_create(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
                azh_runner** out) {
     return guarded([&] {

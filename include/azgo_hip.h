@@ -97,6 +97,12 @@ int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* byt
  * 512 MB (or the test hook's limit). */
 int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_per_hub);
 
+/* The same check for a total already summed over several groups of hubs
+ * (checkCudaInferenceMemory's overload over GpuHubs groups,
+ * src/cuda/cuda_runner.cu:242-256): need_bytes against free memory less
+ * 512 MB; max_batch and hubs only word the message. */
+int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs);
+
 /* makeCudaRunner (include/azgo/cuda.hpp:53-58; src/cuda/cuda_runner.cu:227-234)
  * and CudaWeights::upload (src/cuda/cuda_network.cu:71-106): checks memory,
  * uploads the tensors once (the caller's arrays are not kept), allocates

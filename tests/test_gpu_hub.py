@@ -1,0 +1,35 @@
+"""The backend's C++ adapter (alphazero-go_amd/host/: HipBatchRunner,
+makeHipRunner, HipInference, hip_probe) driven through the REFERENCE's own
+InferenceHub and Network, compiled from the reference's sources together
+with tests/hub_hip_driver.cpp (oracle/Makefile, target hubdriver). This is
+the drop-in proof: the reference's unchanged hub batches many workers' leaf
+requests into passes of this backend.
+
+Scenarios (tests/test_cuda.cpp:1022-1237, tests/test_inference_hub.cpp:272-628):
+chaos batching with 16 workers (every row bit-identical to the position
+alone; logits within maxErr 1e-5 and values within 1e-4 of Network::infer),
+injected failure reaching every later
+request, the memory refusal, argument refusals, and the destructor draining
+a delayed pass whose outputs are on the host when done comes.
+"""
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRIVER = os.path.join(ROOT, "oracle", "_ref", "hub_hip_driver")
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not os.path.exists(DRIVER),
+                       reason="hub driver not built: it compiles the reference's sources (make -C oracle hubdriver)"),
+]
+
+
+@pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain"])
+def test_reference_hub_drives_hip_runner(hip, scenario):
+    r = subprocess.run([DRIVER, scenario], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert f"PASS {scenario}" in r.stdout
