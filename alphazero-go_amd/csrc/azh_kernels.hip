@@ -46,14 +46,19 @@ __device__ inline float epilogue(float acc, float s, float h, const float* skip,
     return v;
 }
 
-// MASKED: input channels past cin are read as zeros (the stem's 2H+2
-// planes); without it every chunk is whole (cin a multiple of 16).
-template <int N, int COW, int WAVES, bool MASKED>
+// A workgroup computes one board's output channels [co tile] at column
+// groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
+// channels and PPW column groups (PPW = 0: all of them). MASKED: input
+// channels past cin are read as zeros (the stem's 2H+2 planes); without it
+// every chunk is whole (cin a multiple of 16).
+template <int N, int COW, int WCO, int WPG, int PPW0, bool MASKED>
 __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
                                             const float* __restrict__ scale, const float* __restrict__ shift,
                                             const float* skip, float* y, int cin, int cout, int nq, int coTiles,
-                                            int relu) {
+                                            int pixTiles, int relu) {
     using G = Geo<N>;
+    constexpr int PPW = PPW0 == 0 ? G::NPG : PPW0;
+    constexpr int WAVES = WCO * WPG;
     constexpr int THREADS = WAVES * 64;
     constexpr int ITEMS = 4 * G::A;   // (channel group, point) pairs per chunk
     constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
@@ -65,8 +70,12 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     const int total = gridDim.x;
     const int wg = blockIdx.x;
     const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
-    const int b = logical / coTiles, ct = logical % coTiles;
-    const int cb0 = (ct * WAVES + wave) * COW;
+    const int tilesPerBoard = coTiles * pixTiles;
+    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
+    const int ct = tile / pixTiles, pt = tile % pixTiles;
+    const int cb0 = (ct * WCO + wave / WPG) * COW;
+    // This wave's first column group (a constant 0 when every wave covers the board).
+    const int pg0 = PPW0 == 0 ? 0 : (pt * WPG + wave % WPG) * PPW;
     const int k = lane >> 4, n16 = lane & 15;
 
     for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -74,12 +83,12 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     // Each lane's LDS read position per column group (float4 units), taps
     // and buffers added as constants. Points past the board read a valid
     // cell; their outputs are never stored.
-    int rofs[G::NPG];
+    int rofs[PPW];
 #pragma unroll
-    for (int pg = 0; pg < G::NPG; ++pg) {
-        int p = pg * 16 + n16;
+    for (int j = 0; j < PPW; ++j) {
+        int p = (pg0 + j) * 16 + n16;
         p = p < G::A ? p : G::A - 1;
-        rofs[pg] = k * G::HA + (p / N) * G::H + (p % N);
+        rofs[j] = k * G::HA + (p / N) * G::H + (p % N);
     }
 
     const float* xb = x + (size_t)b * cin * G::A;
@@ -110,11 +119,11 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         }
     };
 
-    f4 acc[COW][G::NPG];
+    f4 acc[COW][PPW];
 #pragma unroll
     for (int c = 0; c < COW; ++c)
 #pragma unroll
-        for (int pg = 0; pg < G::NPG; ++pg) acc[c][pg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < PPW; ++j) acc[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     load(0);
     __syncthreads();   // the zero fill is complete before any interior store
@@ -128,7 +137,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     // group hints keep that interleave (a step's MFMAs, then the read kRing
     // steps ahead).
     constexpr int kRing = 4;
-    constexpr int STEPS = 9 * G::NPG;
+    constexpr int STEPS = 9 * PPW;
     auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
     auto loadA = [&](int q, int t, f4 (&a)[COW]) {
 #pragma unroll
@@ -141,15 +150,15 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         loadA(q, 0, aCur);
         f4 ring[kRing];
 #pragma unroll
-        for (int i = 0; i < kRing; ++i) ring[i] = buf[rofs[i % G::NPG] + tapOffset(i / G::NPG)];
+        for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = buf[rofs[i % PPW] + tapOffset(i / PPW)];
         __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);   // the ring's first reads
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
-            const int t = i / G::NPG, pg = i % G::NPG;
+            const int t = i / PPW, pg = i % PPW;
             if (pg == 0 && t + 1 < 9) loadA(q, t + 1, aNext);
             const f4 bv = ring[i % kRing];
             if (i + kRing < STEPS)
-                ring[i % kRing] = buf[rofs[(i + kRing) % G::NPG] + tapOffset((i + kRing) / G::NPG)];
+                ring[i % kRing] = buf[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -157,7 +166,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
                     acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
             if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
-            if (pg == G::NPG - 1 && t + 1 < 9) {
+            if (pg == PPW - 1 && t + 1 < 9) {
 #pragma unroll
                 for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
             }
@@ -177,11 +186,11 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
             if (co >= cout) continue;
             const float s = scale[co], h = shift[co];
 #pragma unroll
-            for (int pg = 0; pg < G::NPG; ++pg) {
-                const int p = pg * 16 + n16;
+            for (int j = 0; j < PPW; ++j) {
+                const int p = (pg0 + j) * 16 + n16;
                 if (p < G::A) {
                     const size_t o = (size_t)co * G::A + p;
-                    yb[o] = epilogue(acc[c][pg][r], s, h, skipb ? skipb + o : nullptr, relu != 0);
+                    yb[o] = epilogue(acc[c][j][r], s, h, skipb ? skipb + o : nullptr, relu != 0);
                 }
             }
         }
@@ -190,41 +199,39 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
 
 // The residual tower's convolutions (cin = filters, a multiple of 16) and
 // the stem's (cin = 2H+2 input planes) are separate kernels, so profiles
-// tell them apart.
-template <int N, int COW, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 && WAVES >= 4 ? 2 : 1, COW == 1 && WAVES >= 4 ? 2 : 1)))
-void conv3x3Tower(const float* __restrict__ x, const f4* __restrict__ wp,
-                                                           const float* __restrict__ scale,
-                                                           const float* __restrict__ shift, const float* skip,
-                                                           float* y, int cin, int cout, int nq, int coTiles,
-                                                           int relu) {
-    conv3x3Body<N, COW, WAVES, false>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, relu);
-}
+// tell them apart. Two waves per SIMD are asked for where the whole
+// workgroup shape allows it (one 16-channel block per wave).
+#define AZH_CONV_KERNEL(NAME, MASKED)                                                                      \
+    template <int N, int COW, int WCO, int WPG, int PPW>                                                  \
+    __global__ __launch_bounds__(WCO* WPG * 64)                                                          \
+        __attribute__((amdgpu_waves_per_eu(COW == 1 && WCO * WPG >= 4 ? 2 : 1,                           \
+                                           COW == 1 && WCO * WPG >= 4 ? 2 : 1))) void                    \
+        NAME(const float* __restrict__ x, const f4* __restrict__ wp, const float* __restrict__ scale,      \
+             const float* __restrict__ shift, const float* skip, float* y, int cin, int cout, int nq,      \
+             int coTiles, int pixTiles, int relu) {                                                        \
+        conv3x3Body<N, COW, WCO, WPG, PPW, MASKED>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,   \
+                                                   pixTiles, relu);                                        \
+    }
+AZH_CONV_KERNEL(conv3x3Tower, false)
+AZH_CONV_KERNEL(conv3x3Stem, true)
+#undef AZH_CONV_KERNEL
 
-template <int N, int COW, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(COW == 1 && WAVES >= 4 ? 2 : 1, COW == 1 && WAVES >= 4 ? 2 : 1)))
-void conv3x3Stem(const float* __restrict__ x, const f4* __restrict__ wp,
-                                                          const float* __restrict__ scale,
-                                                          const float* __restrict__ shift, const float* skip,
-                                                          float* y, int cin, int cout, int nq, int coTiles,
-                                                          int relu) {
-    conv3x3Body<N, COW, WAVES, true>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, relu);
-}
-
-template <int N, int COW, int WAVES>
+template <int N, int COW, int WCO, int WPG, int PPW>
 hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
                        float* y, int B, int cin, int cout, bool relu, hipStream_t stream) {
-    const int coTile = 16 * COW * WAVES;
-    const int coTiles = ceilDiv(cout, coTile);
+    constexpr int NPG = Geo<N>::NPG;
+    constexpr int pgPerWave = PPW == 0 ? NPG : PPW;
+    const int coTiles = ceilDiv(cout, 16 * COW * WCO);
+    const int pixTiles = ceilDiv(NPG, WPG * pgPerWave);
     const int nq = ceilDiv(cin, kChunk);
-    const dim3 grid(B * coTiles), block(WAVES * 64);
+    const dim3 grid(B * coTiles * pixTiles), block(WCO * WPG * 64);
     if (cin % kChunk == 0)
-        hipLaunchKernelGGL((conv3x3Tower<N, COW, WAVES>), grid, block, 0, stream, x,
-                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
+        hipLaunchKernelGGL((conv3x3Tower<N, COW, WCO, WPG, PPW>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles, pixTiles,
                            relu ? 1 : 0);
     else
-        hipLaunchKernelGGL((conv3x3Stem<N, COW, WAVES>), grid, block, 0, stream, x,
-                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles,
+        hipLaunchKernelGGL((conv3x3Stem<N, COW, WCO, WPG, PPW>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles, pixTiles,
                            relu ? 1 : 0);
     return hipGetLastError();
 }
@@ -232,12 +239,20 @@ hipError_t launchConvT(const float* x, const float* wp, const float* scale, cons
 template <int N>
 hipError_t launchConvN(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
                        float* y, int B, int cin, int cout, bool relu, ConvTiling t, hipStream_t stream) {
-    if (t.coPerWave == 2 && t.waves == 4) return launchConvT<N, 2, 4>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
-    if (t.coPerWave == 2 && t.waves == 2) return launchConvT<N, 2, 2>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
-    if (t.coPerWave == 1 && t.waves == 4) return launchConvT<N, 1, 4>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
-    if (t.coPerWave == 1 && t.waves == 2) return launchConvT<N, 1, 2>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
-    if (t.coPerWave == 1 && t.waves == 1) return launchConvT<N, 1, 1>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
-    if (t.coPerWave == 1 && t.waves == 8) return launchConvT<N, 1, 8>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+#define AZH_TILE(C, WC, WG, P)                                                                            \
+    if (t.coPerWave == C && t.wavesCo == WC && t.wavesPg == WG && t.pgPerWave == P)                       \
+        return launchConvT<N, C, WC, WG, P>(x, wp, scale, shift, skip, y, B, cin, cout, relu, stream);
+    AZH_TILE(1, 4, 1, 0)
+    AZH_TILE(2, 4, 1, 0)
+    AZH_TILE(1, 2, 1, 0)
+    AZH_TILE(1, 1, 1, 0)
+    AZH_TILE(1, 8, 1, 0)
+    AZH_TILE(1, 2, 2, 12)
+    AZH_TILE(1, 1, 4, 6)
+    AZH_TILE(1, 1, 4, 2)
+    AZH_TILE(1, 1, 4, 1)
+    AZH_TILE(1, 1, 8, 1)
+#undef AZH_TILE
     return hipErrorInvalidValue;
 }
 
@@ -430,17 +445,29 @@ std::vector<float> packConv3x3(const float* w, int cin, int cout) {
 bool conv3x3Supported(int n) { return n == 5 || n == 9 || n == 13 || n == 19; }
 
 ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
-    (void)B;
-    (void)boardSize;
-    // 4 waves of 16 output channels each: 64 per workgroup, so the headline
-    // layer (256 boards x 128 channels) is 512 workgroups, two resident per
-    // CU (226 registers per lane, 56 KB of LDS each), one hiding the other's
-    // staging, barriers and epilogue. Measured fastest of the shapes at
-    // every batch from 1 to 512 on 19x19 and 9x9 boards.
+    // By the layer's count of 16 x 16 output tiles (positions x 16-channel
+    // blocks x 16-point column groups), from measurements on 19x19, 9x9 and
+    // 5x5 boards at batches 1 to 512:
+    // - large layers (the headline 256 boards x 128 channels has 47k tiles):
+    //   4 waves of 16 channels over the whole board, 64 channels per
+    //   workgroup, two workgroups resident per CU (226 registers per lane,
+    //   56 KB of LDS each), one hiding the other's staging, barriers and
+    //   epilogue;
+    // - smaller layers spread a board's column groups over waves and
+    //   workgroups instead, so a batch of 1 at 128 channels still runs 48
+    //   workgroups.
     const int coBlocks = ceilDiv(cout, kCoBlock);
-    if (coBlocks >= 4) return {1, 4};
-    if (coBlocks >= 2) return {1, 2};
-    return {1, 1};
+    const int groups = ceilDiv(boardSize * boardSize, 16);
+    const long tiles = (long)B * coBlocks * groups;
+    if (tiles >= 40000) {
+        if (coBlocks >= 4) return {1, 4, 1, 0};
+        if (coBlocks >= 2) return {1, 2, 1, 0};
+        return {1, 1, 1, 0};
+    }
+    // 4 waves of 6 column groups cover a 19x19 board's 23 in one workgroup.
+    if (groups >= 16 && tiles >= 3072) return {1, 1, 4, 6};
+    if (tiles >= 1024) return {1, 1, 8, 1};
+    return {1, 1, 4, 1};
 }
 
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,

@@ -40,9 +40,12 @@ size_t packedConv3x3Floats(int cin, int cout);
 // channel sums its inputs in one fixed order (chunk, tap, channel-in-chunk),
 // so results are bitwise independent of the cut and of the batch.
 struct ConvTiling {
-    int coPerWave;   // MFMA co blocks per wave: 1 or 2
-    int waves;       // waves per workgroup: 1, 2, 4 or 8 (at most 128 channels)
-    int coTile() const { return 16 * coPerWave * waves; }
+    int coPerWave;   // MFMA blocks of 16 output channels per wave: 1 or 2
+    int wavesCo;     // waves along the output channels (at most 128 channels per workgroup)
+    int wavesPg;     // waves along the board's 16-point column groups
+    int pgPerWave;   // column groups per wave; 0: all of the board's
+    int waves() const { return wavesCo * wavesPg; }
+    int coTile() const { return 16 * coPerWave * wavesCo; }
 };
 ConvTiling chooseConvTiling(int cout, int B, int boardSize);
 

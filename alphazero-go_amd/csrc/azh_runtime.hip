@@ -76,8 +76,9 @@ constexpr size_t kMemoryMargin = size_t(512) << 20;
 // the tree search needs.
 constexpr int kPollFirstUs = 50, kPollLastUs = 200;
 constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
-// The workgroup shapes a probe may force (co blocks per wave, waves).
-const azh::ConvTiling kTilings[] = {{2, 4}, {2, 2}, {1, 4}, {1, 2}, {1, 1}, {1, 8}};
+// The workgroup shapes a probe may force (include/azgo_hip.h lists them).
+const azh::ConvTiling kTilings[] = {{2, 4, 1, 0}, {1, 4, 1, 0},  {1, 2, 1, 0}, {1, 1, 1, 0}, {1, 8, 1, 0},
+                                    {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1}};
 constexpr int kTilingCount = sizeof kTilings / sizeof kTilings[0];
 
 // ---------------------------------------------------------------- context
