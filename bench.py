@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=0, help="override the workload's batch")
     ap.add_argument("--conv-iters", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-calls", type=int, default=16, help="batch-8 passes per CPU worker")
+    ap.add_argument("--cpu-calls", type=int, default=96, help="batch-8 passes per CPU worker")
     return ap.parse_args()
 
 
@@ -147,7 +147,8 @@ def main():
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
     pass_tflops = w.flops_per_position() * B / (ms_per_step * 1e-3) / 1e12
     kernel_hash = azgo_hip.describe().rsplit("kernels ", 1)[-1]
-    traffic = traffic_from_profile(w.name, kernel_hash)
+    name = f"{n}x{n} {blocks}x{F} batch {B}"
+    traffic = traffic_from_profile(name, kernel_hash)
 
     line = {
         "metric": "net evals (positions)/sec at 19x19 batch 256; % fp32-MFMA peak",
@@ -162,7 +163,7 @@ def main():
         "vs_baseline": round(value / REFERENCE_POS_PER_S, 3) if args.workload == 3 and B == 256 else None,
         "dtype": "fp32",
         "data": "synthetic (seeded He-normal weights, synthetic BN statistics, random boards)",
-        "config": {"workload": w.name, "board": n, "blocks": blocks, "filters": F, "value_hidden": V,
+        "config": {"workload": name, "board": n, "blocks": blocks, "filters": F, "value_hidden": V,
                    "global_batch": B, "parallelism": "single GPU"},
         "pct_fp32_mfma_peak": round(100 * pass_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
         "pass_tflops": round(pass_tflops, 2),
