@@ -22,6 +22,10 @@ HEADERS = ["azh_kernels.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # The conv kernels' step streams (up to 9 taps x 23 column groups
+         # per chunk) are unrolled whole; the default size limit for a
+         # pragma-requested unroll stops short of that.
+         "-mllvm", "-pragma-unroll-threshold=100000",
          "-I", os.path.join(ROOT, "include"), "-Wall"]
 
 

@@ -39,9 +39,9 @@ struct Geo {
 };
 
 // y = relu?(scale * acc + shift (+ skip)), each operation rounded on its own.
-__device__ inline float epilogue(float acc, float s, float h, const float* skip, bool relu) {
+__device__ inline float epilogue(float acc, float s, float h, bool addSkip, float skipv, bool relu) {
     float v = __fadd_rn(__fmul_rn(s, acc), h);
-    if (skip) v = __fadd_rn(v, *skip);
+    if (addSkip) v = __fadd_rn(v, skipv);
     if (relu) v = v > 0.0f ? v : 0.0f;   // -0 and NaN become +0 (reluForward)
     return v;
 }
@@ -175,8 +175,36 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         __syncthreads();
     }
 
+    // The residual input may be the output buffer itself (the block's
+    // second convolution writes over its input), so the compiler cannot
+    // move a residual read above an earlier store. All of a lane's residual
+    // values are read first, in one batch, then combined and stored.
     const float* skipb = skip ? skip + (size_t)b * cout * G::A : nullptr;
     float* yb = y + (size_t)b * cout * G::A;
+    float sc[COW][4], sh[COW][4];
+#pragma unroll
+    for (int c = 0; c < COW; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
+            sc[c][r] = scale[co];
+            sh[c][r] = shift[co];
+        }
+    f4 res[COW][PPW];
+    if (skipb) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c)
+#pragma unroll
+            for (int j = 0; j < PPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    // Lanes past the board or past cout read a valid cell;
+                    // their values are never stored.
+                    const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
+                    const int p = min((pg0 + j) * 16 + n16, G::A - 1);
+                    res[c][j][r] = skipb[(size_t)co * G::A + p];
+                }
+    }
 #pragma unroll
     for (int c = 0; c < COW; ++c) {
         const int coBase = (cb0 + c) * 16 + 4 * k;
@@ -184,14 +212,12 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         for (int r = 0; r < 4; ++r) {
             const int co = coBase + r;
             if (co >= cout) continue;
-            const float s = scale[co], h = shift[co];
 #pragma unroll
             for (int j = 0; j < PPW; ++j) {
                 const int p = (pg0 + j) * 16 + n16;
-                if (p < G::A) {
-                    const size_t o = (size_t)co * G::A + p;
-                    yb[o] = epilogue(acc[c][j][r], s, h, skipb ? skipb + o : nullptr, relu != 0);
-                }
+                if (p < G::A)
+                    yb[(size_t)co * G::A + p] =
+                        epilogue(acc[c][j][r], sc[c][r], sh[c][r], skipb != nullptr, res[c][j][r], relu != 0);
             }
         }
     }
@@ -286,9 +312,9 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
         }
     }
     float* ab = act + (size_t)b * 3 * A;
-    ab[p] = epilogue(a0, w.scale[0], w.shift[0], nullptr, true);
-    ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], nullptr, true);
-    ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], nullptr, true);
+    ab[p] = epilogue(a0, w.scale[0], w.shift[0], false, 0.0f, true);
+    ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], false, 0.0f, true);
+    ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], false, 0.0f, true);
 }
 
 // The heads' Linear layers as MFMA GEMMs over 16 positions per workgroup
