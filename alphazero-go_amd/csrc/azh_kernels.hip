@@ -135,7 +135,9 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     // run, and each tap's A fragments are fetched from global memory one tap
     // ahead, so neither read's latency stalls the matrix pipe. The sched
     // group hints keep that interleave (a step's MFMAs, then the read kRing
-    // steps ahead).
+    // steps ahead) and pin each A fetch to the start of the tap before the
+    // one that uses it (left free, the scheduler sinks it next to its use
+    // to save four registers, and every tap then waits a full round trip).
     constexpr int kRing = 4;
     constexpr int STEPS = 9 * PPW;
     auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
@@ -143,11 +145,13 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
 #pragma unroll
         for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
     };
+    f4 aCur[COW], aNext[COW];
+    loadA(0, 0, aCur);
     for (int q = 0; q < nq; ++q) {
-        if (q + 1 < nq) load(q + 1);
+        // The last chunk fetches itself again in place of a next one (never
+        // stored), which keeps the step stream free of branches.
+        const int qn = q + 1 < nq ? q + 1 : q;
         const f4* buf = lds + (q & 1) * G::BUF;
-        f4 aCur[COW], aNext[COW];
-        loadA(q, 0, aCur);
         f4 ring[kRing];
 #pragma unroll
         for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = buf[rofs[i % PPW] + tapOffset(i / PPW)];
@@ -155,7 +159,15 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
             const int t = i / PPW, pg = i % PPW;
-            if (pg == 0 && t + 1 < 9) loadA(q, t + 1, aNext);
+            if (pg == 0) {
+                // The next tap's A fragments (tap 8: the next chunk's first),
+                // and at tap 0 after them the next chunk's board planes: the
+                // count of outstanding loads drains in issue order, so tap
+                // 1's wait for its fragments does not wait for the planes.
+                loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
+                __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);   // issued here, a tap ahead
+                if (t == 0) load(qn);
+            }
             const f4 bv = ring[i % kRing];
             if (i + kRing < STEPS)
                 ring[i % kRing] = buf[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
@@ -166,7 +178,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
                     acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
             if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
-            if (pg == PPW - 1 && t + 1 < 9) {
+            if (pg == PPW - 1) {
 #pragma unroll
                 for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
             }
