@@ -76,7 +76,7 @@ def load():
             "azh_slot_logits": ([vp, C.c_int], f32),
             "azh_slot_values": ([vp, C.c_int], f32),
             "azh_begin": ([vp, C.c_int, C.c_int, DONE_FN, vp], C.c_int),
-            "azh_infer": ([vp, f32, C.c_int, f32, f32], C.c_int),
+            "azh_infer": ([vp, f32, C.c_int, f32, f32, f32], C.c_int),
             "azh_softmax_legal": ([f32, u8, C.c_int, C.c_int, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
@@ -89,7 +89,7 @@ def load():
             "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    f32], C.c_int),
             "azh_time_conv3x3": ([C.c_int] * 6 + [f32], C.c_int),
-            "azh_probe_heads": ([vp, f32, C.c_int, f32, f32], C.c_int),
+            "azh_probe_heads": ([vp, f32, C.c_int, f32, f32, f32], C.c_int),
             "azh_probe_trunk": ([vp, f32, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_fill": ([f32, C.c_size_t, C.c_float, C.c_size_t], C.c_int),
             "azh_probe_copy": ([C.c_size_t, C.c_int, f32], C.c_int),
@@ -185,13 +185,15 @@ class Runner:
     def slots(self):
         return self.lib.azh_slots(self.h)
 
-    def infer(self, inp):
+    def infer(self, inp, ownership=False):
+        """(logits, values), plus ownership [B][area] when asked."""
         inp = _f32(inp)
         B = inp.shape[0]
         logits = np.empty((B, self.cfg.actions), np.float32)
         values = np.empty(B, np.float32)
-        _check(self.lib.azh_infer(self.h, _f(inp), B, _f(logits), _f(values)))
-        return logits, values
+        own = np.empty((B, self.cfg.board * self.cfg.board), np.float32) if ownership else None
+        _check(self.lib.azh_infer(self.h, _f(inp), B, _f(logits), _f(values), _f(own) if ownership else None))
+        return (logits, values, own) if ownership else (logits, values)
 
     def set_graphs(self, enabled):
         _check(self.lib.azh_set_graphs(self.h, int(enabled)))
@@ -257,13 +259,14 @@ class Runner:
         return ms.value
 
     # ---- probes
-    def probe_heads(self, trunk):
+    def probe_heads(self, trunk, ownership=False):
         trunk = _f32(trunk)
         B = trunk.shape[0]
         logits = np.empty((B, self.cfg.actions), np.float32)
         values = np.empty(B, np.float32)
-        _check(self.lib.azh_probe_heads(self.h, _f(trunk), B, _f(logits), _f(values)))
-        return logits, values
+        own = np.empty((B, self.cfg.board * self.cfg.board), np.float32) if ownership else None
+        _check(self.lib.azh_probe_heads(self.h, _f(trunk), B, _f(logits), _f(values), _f(own) if ownership else None))
+        return (logits, values, own) if ownership else (logits, values)
 
     def probe_trunk(self, inp, blocks):
         inp = _f32(inp)

@@ -300,16 +300,19 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 // and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
 // one point per thread, loads hoisted 16 channels ahead of their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
-// src/network.cpp:278-285), plane 2 the value's [A] row.
+// src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
+// ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
+// (src/network.cpp:298-308), into own [B][A].
 template <int N>
 __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const float* __restrict__ trunk,
                                                                           HeadWeights w, float* __restrict__ act,
-                                                                          int F) {
+                                                                          float* __restrict__ own, int F) {
     constexpr int A = N * N;
     const int b = blockIdx.x, p = threadIdx.x;
     if (p >= A) return;
+    const bool withOwn = own != nullptr;
     const float* tb = trunk + (size_t)b * F * A + p;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     for (int c0 = 0; c0 < F; c0 += 16) {
         float xv[16];
 #pragma unroll
@@ -320,6 +323,7 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
                 a0 = fmaf(w.convW[c0 + u], xv[u], a0);
                 a1 = fmaf(w.convW[F + c0 + u], xv[u], a1);
                 a2 = fmaf(w.convW[2 * F + c0 + u], xv[u], a2);
+                if (withOwn) a3 = fmaf(w.convW[3 * F + c0 + u], xv[u], a3);
             }
         }
     }
@@ -327,6 +331,7 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
     ab[p] = epilogue(a0, w.scale[0], w.shift[0], false, 0.0f, true);
     ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], false, 0.0f, true);
     ab[2 * A + p] = epilogue(a2, w.scale[2], w.shift[2], false, 0.0f, true);
+    if (withOwn) own[(size_t)b * A + p] = tanhf(epilogue(a3, w.scale[3], w.shift[3], false, 0.0f, false));
 }
 
 // The heads' Linear layers as MFMA GEMMs over 16 positions per workgroup
@@ -521,8 +526,8 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
     }
 }
 
-hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values, int B,
-                       int n, int F, int V, hipStream_t stream) {
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values,
+                       float* own, int B, int n, int F, int V, hipStream_t stream) {
     if (B < 1) return hipSuccess;
     if (V > 256) return hipErrorInvalidValue;
     const int A1 = n * n + 1;
@@ -531,7 +536,7 @@ hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, flo
     switch (n) {
 #define AZH_HEADS(NN)                                                                                         \
     case NN:                                                                                                  \
-        hipLaunchKernelGGL(headConvKernel<NN>, grid1, block1, 0, stream, trunk, w, act, F);                  \
+        hipLaunchKernelGGL(headConvKernel<NN>, grid1, block1, 0, stream, trunk, w, act, own, F);             \
         hipLaunchKernelGGL(headFcKernel<NN>, grid2, block2, 0, stream, act, w, logits, values, B, V);        \
         break;
         AZH_HEADS(5)

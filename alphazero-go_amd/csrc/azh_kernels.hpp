@@ -59,15 +59,16 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
                          hipStream_t stream);
 bool conv3x3Supported(int boardSize);
 
-// The policy and value heads (src/network.cpp:274-296), two kernels: the
-// 1x1 convs F -> 2 and F -> 1 with BN and ReLU, one position per workgroup,
-// into act [B][3][n*n]; then the policy Linear (2A -> A+1) and the value
-// Linears (A -> V, ReLU, V -> 1) and tanh as MFMA GEMMs, 16 positions per
-// workgroup. V at most 256.
+// The heads (src/network.cpp:274-308), two kernels: the 1x1 convs F -> 2
+// (policy) and F -> 1 (value) with BN and ReLU, one position per workgroup,
+// into act [B][3][n*n], and, when the network has it, the ownership head's
+// 1x1 conv F -> 1 with BN and tanh straight into own [B][n*n]; then the
+// policy Linear (2A -> A+1) and the value Linears (A -> V, ReLU, V -> 1) and
+// tanh as MFMA GEMMs, 16 positions per workgroup. V at most 256.
 struct HeadWeights {
-    const float* convW;      // [3][F]: policy rows 0-1, value row 2
-    const float* scale;      // [3] folded BN scale
-    const float* shift;      // [3] folded BN shift
+    const float* convW;      // [4][F]: policy rows 0-1, value row 2, ownership row 3
+    const float* scale;      // [4] folded BN scale
+    const float* shift;      // [4] folded BN shift
     const float* policyWT;   // [pad16(2A)][pad16(A+1)]: policy.fc.w transposed, zero-padded
     const float* policyB;    // [A+1]
     const float* fc1WT;      // [pad16(A)][pad16(V)]: value.fc1.w transposed, zero-padded
@@ -77,8 +78,8 @@ struct HeadWeights {
 };
 size_t headPolicyWTFloats(int n);
 size_t headFc1WTFloats(int n, int V);
-hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values, int B,
-                       int n, int F, int V, hipStream_t stream);
+hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values,
+                       float* own, int B, int n, int F, int V, hipStream_t stream);
 
 // priors[b][a] = exp(l - max) / sum over legal a of the same, 0 where
 // illegal (Mcts::expand's softmax, src/mcts.cpp:170-183). One wavefront per

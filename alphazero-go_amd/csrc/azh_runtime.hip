@@ -147,9 +147,10 @@ void requireContext() {
 
 struct Shape {
     int n, H, P, A, A1, F, V, blocks;
+    bool ownership;
     explicit Shape(const azh_netcfg& c)
         : n(c.board), H(c.history), P(2 * c.history + 2), A(c.board * c.board), A1(c.board * c.board + 1),
-          F(c.filters), V(c.value_hidden), blocks(c.blocks) {}
+          F(c.filters), V(c.value_hidden), blocks(c.blocks), ownership(c.ownership != 0) {}
 };
 
 void validate(const azh_netcfg* c) {
@@ -159,8 +160,6 @@ void validate(const azh_netcfg* c) {
     if (c->history < 1 || c->blocks < 0 || c->filters < 1 || c->value_hidden < 1)
         throw Error(AZH_ERR_ARGUMENT, "hip: invalid network config");
     if (c->value_hidden > 256) throw Error(AZH_ERR_ARGUMENT, "hip: value_hidden above 256 not supported");
-    if (c->ownership)
-        throw Error(AZH_ERR_ARGUMENT, "hip: the ownership head is not part of this backend's pass");
 }
 
 // Network::params() then Network::buffers() (src/network.cpp:113-165).
@@ -195,6 +194,10 @@ std::vector<TensorSpec> tensorSpec(const azh_netcfg& c) {
     t.push_back({"value.fc1.b", (size_t)s.V});
     t.push_back({"value.fc2.w", (size_t)s.V});
     t.push_back({"value.fc2.b", 1});
+    if (s.ownership) {
+        t.push_back({"ownership.conv.w", F});
+        bn("ownership.bn", 1);
+    }
     auto stats = [&](const std::string& p, size_t ch) {
         t.push_back({p + ".runMean", ch});
         t.push_back({p + ".runVar", ch});
@@ -207,6 +210,7 @@ std::vector<TensorSpec> tensorSpec(const azh_netcfg& c) {
     }
     stats("policy.bn", 2);
     stats("value.bn", 1);
+    if (s.ownership) stats("ownership.bn", 1);
     return t;
 }
 
@@ -236,7 +240,7 @@ size_t weightFloats(const azh_netcfg& c) {
     size_t f = 0;
     f += alignFloats(azh::packedConv3x3Floats(s.P, s.F)) + 2 * alignFloats(s.F);
     f += (size_t)s.blocks * 2 * (alignFloats(azh::packedConv3x3Floats(s.F, s.F)) + 2 * alignFloats(s.F));
-    f += alignFloats(3 * s.F) + 2 * alignFloats(3);
+    f += alignFloats(4 * s.F) + 2 * alignFloats(4);
     f += alignFloats(azh::headPolicyWTFloats(s.n)) + alignFloats(s.A1);
     f += alignFloats(azh::headFc1WTFloats(s.n, s.V)) + alignFloats(s.V) + alignFloats(s.V) + alignFloats(1);
     return f;
@@ -311,13 +315,19 @@ void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*
         c1.push_back(conv(p + ".conv1.w", p + ".bn1", s.F));
         c2.push_back(conv(p + ".conv2.w", p + ".bn2", s.F));
     }
-    const size_t hConv = take(3 * s.F), hScale = take(3), hShift = take(3);
+    // The heads' 1x1 rows: policy 0-1, value 2, ownership 3 (zero without the head).
+    const size_t hConv = take(4 * s.F), hScale = take(4), hShift = take(4);
     std::copy(T("policy.conv.w"), T("policy.conv.w") + 2 * s.F, host.begin() + hConv);
     std::copy(T("value.conv.w"), T("value.conv.w") + s.F, host.begin() + hConv + 2 * s.F);
     foldBn(T("policy.bn.gamma"), T("policy.bn.beta"), T("policy.bn.runMean"), T("policy.bn.runVar"), 2,
            &host[hScale], &host[hShift]);
     foldBn(T("value.bn.gamma"), T("value.bn.beta"), T("value.bn.runMean"), T("value.bn.runVar"), 1,
            &host[hScale + 2], &host[hShift + 2]);
+    if (s.ownership) {
+        std::copy(T("ownership.conv.w"), T("ownership.conv.w") + s.F, host.begin() + hConv + 3 * s.F);
+        foldBn(T("ownership.bn.gamma"), T("ownership.bn.beta"), T("ownership.bn.runMean"), T("ownership.bn.runVar"),
+               1, &host[hScale + 3], &host[hShift + 3]);
+    }
     // The head Linears transposed ([in][out]) and zero-padded to whole 16 x 16
     // MFMA blocks.
     const size_t np = azh::headPolicyWTFloats(s.n) / (size_t)((2 * s.A + 15) / 16 * 16);
@@ -354,7 +364,7 @@ void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*
 size_t slotFloats(const Shape& s, int maxBatch) {
     const size_t B = maxBatch;
     return alignFloats(B * s.P * s.A) + 2 * alignFloats(B * s.F * s.A) + alignFloats(B * 3 * s.A) +
-           alignFloats(B * s.A1) + alignFloats(B);
+           alignFloats(B * s.A1) + alignFloats(B) + (s.ownership ? alignFloats(B * s.A) : 0);
 }
 
 size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
@@ -366,6 +376,7 @@ struct Slot {
     hipEvent_t event = nullptr;
     float* dev = nullptr;
     float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dAct = nullptr, *dLogits = nullptr, *dValues = nullptr;
+    float* dOwn = nullptr;   // [B][A] after tanh, only with the ownership head
     float *hIn = nullptr, *hLogits = nullptr, *hValues = nullptr;
     std::map<int, hipGraphExec_t> graphs;
     bool busy = false;
@@ -387,6 +398,7 @@ struct Slot {
         dAct = take(B * 3 * s.A);
         dLogits = take(B * s.A1);
         dValues = take(B);
+        if (s.ownership) dOwn = take(B * s.A);
         check(hipHostMalloc((void**)&hIn, B * s.P * s.A * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
         check(hipHostMalloc((void**)&hLogits, B * s.A1 * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
         check(hipHostMalloc((void**)&hValues, B * sizeof(float), hipHostMallocDefault), "hipHostMalloc");
@@ -503,7 +515,8 @@ struct azh_runner {
                   "conv3x3 (conv2)");
         }
         if (heads)
-            check(azh::launchHeads(s.dX, weights.heads, s.dAct, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, stream),
+            check(azh::launchHeads(s.dX, weights.heads, s.dAct, s.dLogits, s.dValues, s.dOwn, B, sh.n, sh.F, sh.V,
+                                   stream),
                   "heads");
     }
 
@@ -729,15 +742,20 @@ int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user) {
     });
 }
 
-int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values) {
+int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership) {
     return guarded([&] {
         if (!r || !input || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: infer needs its arrays");
+        if (ownership && !r->shape.ownership) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no ownership head");
         r->checkBatch(B);
         Slot& s = r->idleSlot(0);
         std::memcpy(s.hIn, input, (size_t)B * r->shape.P * r->shape.A * sizeof(float));
         r->copyIn(s, B);
         r->enqueuePass(s, B);
         r->copyOut(s, B);
+        if (ownership)
+            check(hipMemcpyAsync(ownership, s.dOwn, (size_t)B * r->shape.A * sizeof(float), hipMemcpyDeviceToHost,
+                                 s.stream),
+                  "hipMemcpyAsync(ownership)");
         check(hipStreamSynchronize(s.stream), "GPU inference failed");
         std::memcpy(logits, s.hLogits, (size_t)B * r->shape.A1 * sizeof(float));
         std::memcpy(values, s.hValues, (size_t)B * sizeof(float));
@@ -957,18 +975,23 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
     });
 }
 
-int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values) {
+int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values, float* ownership) {
     return guarded([&] {
         if (!r || !trunk || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: bad heads probe arguments");
+        if (ownership && !r->shape.ownership) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no ownership head");
         r->checkBatch(B);
         Slot& s = r->idleSlot(0);
         const Shape& sh = r->shape;
         check(hipMemcpyAsync(s.dX, trunk, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
-        check(azh::launchHeads(s.dX, r->weights.heads, s.dAct, s.dLogits, s.dValues, B, sh.n, sh.F, sh.V, s.stream),
+        check(azh::launchHeads(s.dX, r->weights.heads, s.dAct, s.dLogits, s.dValues, s.dOwn, B, sh.n, sh.F, sh.V,
+                               s.stream),
               "heads");
         check(hipMemcpyAsync(logits, s.dLogits, (size_t)B * sh.A1 * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");
+        if (ownership)
+            check(hipMemcpyAsync(ownership, s.dOwn, (size_t)B * sh.A * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+                  "hipMemcpyAsync");
         check(hipMemcpyAsync(values, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");
         check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");

@@ -49,7 +49,8 @@ public:
     ~HipInference();
     HipInference(const HipInference&) = delete;
     HipInference& operator=(const HipInference&) = delete;
-    // Network::infer's arguments; the ownership head is not supported.
+    // Network::infer's arguments; ownership needs a network with the head
+    // (std::invalid_argument otherwise, as CudaInference).
     void infer(const float* input, int B, float* logits, float* values, float* ownership = nullptr);
 private:
     struct Impl;

@@ -156,9 +156,9 @@ HipInference::HipInference(const Network& net, int maxBatch) : impl_(new Impl) {
 HipInference::~HipInference() = default;
 
 void HipInference::infer(const float* input, int B, float* logits, float* values, float* ownership) {
-    if (ownership) throw std::invalid_argument("hip: the ownership head is not part of this backend's pass");
-    if (azh_infer(impl_->runner, input, B, logits, values) != AZH_OK)
-        throw std::runtime_error(std::string("GPU inference failed: ") + azh_last_error());
+    const int rc = azh_infer(impl_->runner, input, B, logits, values, ownership);
+    if (rc == AZH_ERR_ARGUMENT) throw std::invalid_argument(azh_last_error());
+    if (rc != AZH_OK) throw std::runtime_error(std::string("GPU inference failed: ") + azh_last_error());
 }
 
 namespace hip_probe {

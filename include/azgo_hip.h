@@ -39,16 +39,16 @@ enum {
     AZH_ERR_STATE = -6        /* a call the runner's state does not allow */
 };
 
-/* NetConfig (include/azgo/network.hpp:24-36). ownership must be 0: the
- * ownership head is not part of this backend's pass (its tensors would be
- * refused as unread). */
+/* NetConfig (include/azgo/network.hpp:24-36). With ownership set the pass
+ * also runs the ownership head (1x1 conv, BN, tanh per point,
+ * src/network.cpp:298-308) and the network's tensors include it. */
 typedef struct azh_netcfg {
     int board;        /* n: 5, 9, 13 or 19 */
     int history;      /* H: planes = 2H + 2 */
     int blocks;       /* residual blocks */
     int filters;      /* F */
     int value_hidden; /* V, at most 256 */
-    int ownership;
+    int ownership;    /* 1: the network has the ownership head */
 } azh_netcfg;
 
 /* One named tensor of Network::params() / buffers() (src/network.cpp:113-165),
@@ -140,8 +140,10 @@ int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user);
 
 /* CudaInference::infer (include/azgo/cuda.hpp:68-84;
  * src/cuda/cuda_network.cu:314-339): the whole pass synchronously on slot
- * 0's resources; the slot must be idle. */
-int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values);
+ * 0's resources; the slot must be idle. ownership [B][area] (after tanh) may
+ * be NULL; non-NULL for a network without the head is AZH_ERR_ARGUMENT, as
+ * CudaInference refuses it. */
+int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership);
 
 /* The legal-move softmax on the GPU (no reference counterpart on the GPU; it
  * restates Mcts::expand's priors, src/mcts.cpp:170-183): priors[b][a] =
@@ -194,9 +196,10 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
  * total ms. For tuning the workgroup shape. */
 int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, float* ms);
 
-/* The heads kernel alone on the runner's weights: trunk [B][F][n*n] ->
- * logits, values. */
-int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values);
+/* The heads kernels alone on the runner's weights: trunk [B][F][n*n] ->
+ * logits, values, and ownership [B][n*n] when non-NULL (the network must
+ * have the head). */
+int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, float* values, float* ownership);
 
 /* The stem and the first `blocks` residual blocks on the runner's weights:
  * input [B][planes][n*n] -> trunk [B][F][n*n]. */

@@ -4,9 +4,10 @@
 // scenarios follow the reference's runner and hub tests
 // (tests/test_cuda.cpp:1022-1237, tests/test_inference_hub.cpp:272-628).
 //
-//   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain
+//   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain | ownership
 //
 // Prints "PASS <scenario>" and exits 0, or prints what failed and exits 1.
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
@@ -18,6 +19,7 @@
 #include <thread>
 #include <vector>
 
+#include "azgo/backend.hpp"
 #include "azgo/inference_hub.hpp"
 #include "azgo/network.hpp"
 #include "azgo/rng.hpp"
@@ -231,16 +233,16 @@ void refusals() {
         threw = true;
     }
     expect(threw, "3 slots refused");
-    NetConfig own = cfg;
-    own.ownership = true;
-    const Network ownNet(own, 31);
     threw = false;
     try {
-        makeHipRunner(ownNet, 8, 2);
+        HipInference gpu(net, 4);
+        std::vector<float> x(4 * static_cast<size_t>(cfg.planes()) * cfg.area(), 0.0f);
+        std::vector<float> l(4 * static_cast<size_t>(cfg.actions())), v(4), o(4 * static_cast<size_t>(cfg.area()));
+        gpu.infer(x.data(), 4, l.data(), v.data(), o.data());
     } catch (const std::invalid_argument& e) {
         threw = std::string(e.what()).find("ownership") != std::string::npos;
     }
-    expect(threw, "a network with the ownership head refused, by name");
+    expect(threw, "ownership asked of a network without the head refused, by name");
     std::unique_ptr<BatchRunner> r = makeHipRunner(net, 8, 1);
     threw = false;
     try {
@@ -283,11 +285,42 @@ void drain() {
     expect(outputsReady, "the outputs were on the host when done came");
 }
 
+// The ownership head through CudaInference::infer's contract
+// (src/cuda/cuda_network.cu:314-339), against the reference's own
+// Network::infer on its naive backend, compiled from its sources.
+void ownership() {
+    NetConfig cfg = config(9, 2, 16, 16);
+    cfg.ownership = true;
+    const Network net = randomNetwork(cfg, 51);
+    Rng rng(52);
+    const int B = 6;
+    const std::vector<float> in = randomPositions(cfg, B, rng);
+    const size_t nl = static_cast<size_t>(B) * cfg.actions(), no = static_cast<size_t>(B) * cfg.area();
+    std::vector<float> rl(nl), rv(B), ro(no), gl(nl), gv(B), go(no);
+    std::unique_ptr<Backend> naive = makeBackend("naive", 1);
+    Workspace ws(cfg, B, *naive);
+    net.infer(ws, in.data(), B, rl.data(), rv.data(), ro.data());
+    HipInference gpu(net, B);
+    gpu.infer(in.data(), B, gl.data(), gv.data(), go.data());
+    double dOwn = 0, dVal = 0, dLog = 0, maxLog = 0;
+    for (size_t i = 0; i < no; ++i) dOwn = std::max(dOwn, (double)std::fabs(go[i] - ro[i]));
+    for (int b = 0; b < B; ++b) dVal = std::max(dVal, (double)std::fabs(gv[b] - rv[b]));
+    for (size_t i = 0; i < nl; ++i) {
+        dLog = std::max(dLog, (double)std::fabs(gl[i] - rl[i]));
+        maxLog = std::max(maxLog, (double)std::fabs(rl[i]));
+    }
+    std::printf("ownership: max-abs ownership %.3g, values %.3g, logits %.3g (|logit| up to %.3g)\n", dOwn, dVal,
+                dLog, maxLog);
+    expect(dOwn <= 1e-4, "ownership within 1e-4 of the reference's Network::infer");
+    expect(dVal <= 1e-4, "values within 1e-4 of the reference's Network::infer");
+    expect(dLog <= 1e-4 * std::max(1.0, maxLog), "logits within 1e-4 (relative to the largest) of Network::infer");
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
     if (argc != 2) {
-        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain\n");
+        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership\n");
         return 2;
     }
     std::string why;
@@ -301,6 +334,7 @@ int main(int argc, char** argv) {
         else if (s == "failure") failure();
         else if (s == "memory") memory();
         else if (s == "refusals") refusals();
+        else if (s == "ownership") ownership();
         else if (s == "drain") drain();
         else {
             std::printf("unknown scenario %s\n", s.c_str());

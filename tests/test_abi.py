@@ -57,8 +57,7 @@ def test_memory_need_formula():
 
 
 @pytest.mark.parametrize("bad", [
-    dict(board=7), dict(board=19, history=0), dict(filters=0), dict(value_hidden=300), dict(ownership=1),
-    dict(blocks=-1),
+    dict(board=7), dict(board=19, history=0), dict(filters=0), dict(value_hidden=300), dict(blocks=-1),
 ])
 def test_config_validation(bad):
     base = dict(board=9, history=8, blocks=2, filters=16, value_hidden=8, ownership=0)
@@ -84,14 +83,38 @@ def test_upload_refuses_unknown_tensor_by_name():
 
 
 def test_upload_refuses_unread_tensor():
-    """tests/test_cuda.cpp:934-947: a tensor of a network the pass does not
-    run (the ownership head) is refused, by name."""
+    """tests/test_cuda.cpp:934-947: a tensor of a head the config does not
+    have (the ownership head's, given for a network without it) is refused,
+    by name."""
     cfg = O.make_cfg(9, 1, 16, 8, ownership=1)
     t = _tensors(cfg)
     plain = to_hip_cfg(azgo_hip, O.make_cfg(9, 1, 16, 8))
     with pytest.raises(azgo_hip.HipError) as e:
         azgo_hip.Runner(plain, t, 4)
     assert e.value.code == azgo_hip.ERR_TENSOR and "ownership" in str(e.value)
+
+
+def test_ownership_network_tensors():
+    """With the head in the config its tensors are the network's own (the
+    host-side check passes, then the runner needs a GPU); without them the
+    first missing one is named."""
+    cfg = O.make_cfg(9, 1, 16, 8, ownership=1)
+    hcfg = to_hip_cfg(azgo_hip, cfg)
+    if not azgo_hip.available()[0]:
+        with pytest.raises(azgo_hip.HipError) as e:
+            azgo_hip.Runner(hcfg, _tensors(cfg), 4)
+        assert e.value.code == azgo_hip.ERR_UNAVAILABLE
+    t = dict(_tensors(cfg))
+    del t["ownership.bn.runVar"]
+    with pytest.raises(azgo_hip.HipError) as e:
+        azgo_hip.Runner(hcfg, t, 4)
+    assert e.value.code == azgo_hip.ERR_TENSOR and "ownership.bn.runVar" in str(e.value)
+    # The slot's extra [B][A] ownership buffer.
+    plain = to_hip_cfg(azgo_hip, O.make_cfg(9, 1, 16, 8))
+    al = lambda f: (f + 63) // 64 * 64   # noqa: E731
+    d_slot = (azgo_hip.memory_need(hcfg, 64, 2) - azgo_hip.memory_need(hcfg, 64, 1)) - \
+             (azgo_hip.memory_need(plain, 64, 2) - azgo_hip.memory_need(plain, 64, 1))
+    assert d_slot == 4 * al(64 * 81)
 
 
 def test_upload_refuses_missing_and_wrong_size():

@@ -9,8 +9,10 @@ Scenarios (tests/test_cuda.cpp:1022-1237, tests/test_inference_hub.cpp:272-628):
 chaos batching with 16 workers (every row bit-identical to the position
 alone; logits within maxErr 1e-5 and values within 1e-4 of Network::infer),
 injected failure reaching every later
-request, the memory refusal, argument refusals, and the destructor draining
-a delayed pass whose outputs are on the host when done comes.
+request, the memory refusal, argument refusals, the destructor draining
+a delayed pass whose outputs are on the host when done comes, and the
+ownership head through HipInference against the reference's own
+Network::infer (naive backend) on a network with the head.
 """
 import os
 import subprocess
@@ -27,7 +29,7 @@ pytestmark = [
 ]
 
 
-@pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain"])
+@pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain", "ownership"])
 def test_reference_hub_drives_hip_runner(hip, scenario):
     r = subprocess.run([DRIVER, scenario], capture_output=True, text=True, timeout=120)
     print(r.stdout)

@@ -212,6 +212,58 @@ def test_heads_probe_vs_oracle(hip):
     assert np.abs(values - ref_values).max() <= 1e-5
 
 
+@pytest.mark.parametrize("cfg,B", [
+    (O.make_cfg(5, 2, 32, ownership=1), 8),
+    (O.make_cfg(9, 2, 16, 8, ownership=1), 7),
+    (O.make_cfg(19, 2, 48, ownership=1), 4),
+])
+def test_ownership_head_vs_oracle(hip, cfg, B):
+    """The ownership head (src/network.cpp:298-308: 1x1 conv F -> 1, BN, tanh
+    at every point) through CudaInference::infer's contract: against the
+    blas restatement (1e-4) and the double pass (within twice the CPU's own
+    gap); the same pass's logits and values are bit for bit those of the
+    network without the head, and asking a network without it for ownership
+    is an argument error (src/cuda/cuda_network.cu:316)."""
+    net = O.random_network(cfg, 90 + cfg.board)
+    rng = np.random.default_rng(91)
+    inp = rng.integers(0, 2, (B, cfg.planes, cfg.area)).astype(np.float32)
+    with _runner(hip, net, B) as r:
+        logits, values, own = r.infer(inp, ownership=True)
+        again = r.infer(inp)
+    blas = O.forward(net, inp, O.BLAS, ownership=True)
+    dbl = O.forward_double(net, inp, ownership=True)
+    gpu_gap = float(np.abs(own.astype(np.float64) - dbl[2]).max())
+    cpu_gap = float(np.abs(blas[2].astype(np.float64) - dbl[2]).max())
+    print(f"{cfg}: ownership gap to double {gpu_gap:.3g} (blas {cpu_gap:.3g})")
+    assert own.shape == (B, cfg.area) and np.isfinite(own).all()
+    assert float(np.abs(own - blas[2]).max()) <= 1e-4
+    assert gpu_gap <= max(1e-5, 2 * cpu_gap)
+    assert bitwise_equal(again[0], logits) and bitwise_equal(again[1], values)
+    plain = O.make_cfg(cfg.board, cfg.blocks, cfg.filters, cfg.value_hidden)
+    tensors = {k: v for k, v in net.tensors().items() if not k.startswith("ownership.")}
+    with hip.Runner(to_hip_cfg(hip, plain), tensors, B) as r:
+        base = r.infer(inp)
+        with pytest.raises(hip.HipError) as e:
+            r.infer(inp, ownership=True)
+        assert e.value.code == hip.ERR_ARGUMENT
+    assert bitwise_equal(base[0], logits) and bitwise_equal(base[1], values)
+
+
+def test_ownership_heads_probe_vs_double(hip):
+    """The heads kernels alone with the ownership head on a given trunk:
+    tanh(bn(w . x)) per point against float64."""
+    cfg = O.make_cfg(19, 1, 32, ownership=1)
+    net = O.random_network(cfg, 83)
+    trunk = np.random.default_rng(84).uniform(0, 2, (3, 32, 361)).astype(np.float32)
+    with _runner(hip, net, 3) as r:
+        _, _, own = r.probe_heads(trunk, ownership=True)
+    t = {k: v.astype(np.float64) for k, v in net.tensors().items()}
+    conv = np.einsum("c,bcp->bp", t["ownership.conv.w"], trunk.astype(np.float64))
+    scale = t["ownership.bn.gamma"][0] / np.sqrt(t["ownership.bn.runVar"][0] + np.float64(np.float32(1e-5)))
+    ref = np.tanh((conv - t["ownership.bn.runMean"][0]) * scale + t["ownership.bn.beta"][0])
+    assert float(np.abs(own - ref).max()) <= 1e-5
+
+
 def test_softmax_legal_vs_oracle(hip):
     """Mcts::expand's priors (src/mcts.cpp:170-183), restated in the oracle."""
     w = O.WORKLOADS[3]
