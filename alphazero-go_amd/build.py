@@ -17,7 +17,13 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libazgo_hip.so")
 SOURCES = ["azh_kernels.hip", "azh_runtime.hip"]
-HEADERS = ["azh_kernels.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
+# The 3x3 convolution is one template instantiated per (board size,
+# workgroup shape): azh_conv_inst.hip is compiled once per pair, so the
+# fully unrolled kernels build in parallel.
+CONV_INST = "azh_conv_inst.hip"
+CONV_HEADERS = ["azh_conv.hpp", "azh_kernels.hpp"]
+BOARD_SIZES = (5, 9, 13, 19)   # conv3x3Supported
+HEADERS = CONV_HEADERS + [os.path.join("..", "..", "include", "azgo_hip.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -29,34 +35,60 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-I", os.path.join(ROOT, "include"), "-Wall"]
 
 
-def kernel_hash():
-    """A hash of the kernel sources, headers and flags: two builds whose
-    hashes match run the same GPU arithmetic."""
+def _hash(files):
     h = hashlib.sha256()
-    for f in SOURCES + HEADERS:
+    for f in files:
         with open(os.path.join(CSRC, f), "rb") as fh:
             h.update(fh.read())
     h.update(" ".join(FLAGS).encode())
     return h.hexdigest()[:8]
 
 
-def build(verbose=False):
+def kernel_hash():
+    """A hash of every kernel source, header and flag: two builds whose
+    hashes match run the same GPU arithmetic."""
+    return _hash(SOURCES + [CONV_INST] + HEADERS)
+
+
+def conv_hash():
+    """The same over the 3x3 convolution's sources only: a profile of the
+    convolution stays valid while this matches."""
+    return _hash([CONV_INST] + CONV_HEADERS)
+
+
+def conv_tiling_count():
+    """Entries of kConvTilings (azh_kernels.hpp)."""
+    text = open(os.path.join(CSRC, "azh_kernels.hpp")).read()
+    body = text[text.index("kConvTilings[] = {") + len("kConvTilings[] = {"):]
+    body = body[:body.index("};")]
+    return body.count("{")
+
+
+def build(verbose=False, jobs=None):
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    defs = [f'-DAZH_KERNEL_HASH="{kernel_hash()}"']
+    defs = [f'-DAZH_KERNEL_HASH="{kernel_hash()}"', f'-DAZH_CONV_HASH="{conv_hash()}"']
+    units = [(src, src.replace(".hip", ".o"), []) for src in SOURCES]
+    for n in BOARD_SIZES:
+        for t in range(conv_tiling_count()):
+            units.append((CONV_INST, f"azh_conv_{n}_{t}.o", [f"-DAZH_CONV_N={n}", f"-DAZH_CONV_TILING={t}"]))
 
-    def compile_one(src):
-        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-        cmd = [HIPCC] + FLAGS + defs + ["-c", os.path.join(CSRC, src), "-o", obj]
+    def compile_one(unit):
+        src, obj_name, extra = unit
+        obj = os.path.join(build_dir, obj_name)
+        cmd = [HIPCC] + FLAGS + defs + extra + ["-c", os.path.join(CSRC, src), "-o", obj]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+            raise RuntimeError(f"hipcc failed for {src} {' '.join(extra)}:\n{r.stderr}")
         if verbose and r.stderr.strip():
             print(r.stderr, file=sys.stderr)
         return obj
 
-    with ThreadPoolExecutor(len(SOURCES)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+    jobs = jobs or max(1, min(16, os.cpu_count() or 1))
+    # Biggest units first (19x19 instances), so the pool ends evenly.
+    units.sort(key=lambda u: 0 if "N=19" in " ".join(u[2]) else 1)
+    with ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(compile_one, units))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,272 @@
+// The gfx950 3x3 convolution (template body; instantiated per board size
+// and workgroup shape by azh_conv_inst.hip).
+//
+// conv3x3: the stem and residual-tower convolutions as an implicit GEMM on
+// fp32 MFMA (v_mfma_f32_16x16x4_f32), no im2col buffer. A workgroup owns one
+// position (board) and a tile of output channels. For each chunk of 16
+// input channels it stages the board's planes in LDS with a one-point zero
+// halo ((n+2) x (n+2) per channel, four channels interleaved per point so a
+// lane fetches four K values with one ds_read_b128); the nine taps are then
+// constant offsets into that tile, so the inner loop is LDS reads with
+// immediate offsets and MFMAs, and the im2col matrix never exists. The
+// chunks are double-buffered: the next chunk's global loads are in flight
+// while the current one is multiplied. Weights come pre-packed in MFMA
+// fragment order straight from global memory (one coalesced dwordx4 per lane
+// per fragment quad; every workgroup reads the same 0.6 MB per layer, which
+// stays in L2). BN (scale, shift), the residual add and ReLU are applied to
+// the accumulators before the single store.
+//
+// MFMA operand layout (16x16x4 f32, wave64): A[i][k] comes from lane
+// i + 16k, B[k][j] from lane j + 16k, and lane j + 16g holds D[4g + r][j] in
+// accumulator element r.
+#pragma once
+#include "azh_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace azh {
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+struct Geo {
+    static constexpr int A = N * N;            // points per plane
+    static constexpr int H = N + 2;            // haloed row length
+    static constexpr int HA = H * H;           // haloed plane (float4 units per group)
+    static constexpr int NPG = (A + 15) / 16;  // 16-point MFMA column groups
+    static constexpr int BUF = 4 * HA;         // float4 units of one LDS buffer (4 groups)
+};
+
+// A workgroup computes one board's output channels [co tile] at column
+// groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
+// channels and PPW column groups (PPW = 0: all of them). MASKED: input
+// channels past cin are read as zeros (the stem's 2H+2 planes); without it
+// every chunk is whole (cin a multiple of 16).
+template <int N, int COW, int WCO, int WPG, int PPW0, bool MASKED>
+__device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
+                                            const float* __restrict__ scale, const float* __restrict__ shift,
+                                            const float* skip, float* y, int cin, int cout, int nq, int coTiles,
+                                            int pixTiles, int relu) {
+    using G = Geo<N>;
+    constexpr int PPW = PPW0 == 0 ? G::NPG : PPW0;
+    constexpr int WAVES = WCO * WPG;
+    constexpr int THREADS = WAVES * 64;
+    constexpr int ITEMS = 4 * G::A;   // (channel group, point) pairs per chunk
+    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
+    __shared__ f4 lds[2 * G::BUF];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
+    // co tiles of one board run on the same XCD and share its L2.
+    const int total = gridDim.x;
+    const int wg = blockIdx.x;
+    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
+    const int tilesPerBoard = coTiles * pixTiles;
+    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
+    const int ct = tile / pixTiles, pt = tile % pixTiles;
+    const int cb0 = (ct * WCO + wave / WPG) * COW;
+    // This wave's first column group (a constant 0 when every wave covers the board).
+    const int pg0 = PPW0 == 0 ? 0 : (pt * WPG + wave % WPG) * PPW;
+    const int k = lane >> 4, n16 = lane & 15;
+
+    for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Each lane's LDS read position per column group (float4 units), taps
+    // and buffers added as constants. Points past the board read a valid
+    // cell; their outputs are never stored.
+    int rofs[PPW];
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) {
+        int p = (pg0 + j) * 16 + n16;
+        p = p < G::A ? p : G::A - 1;
+        rofs[j] = k * G::HA + (p / N) * G::H + (p % N);
+    }
+
+    const float* xb = x + (size_t)b * cin * G::A;
+    f4 stage[PER];
+    auto load = [&](int q) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                const int c0 = q * 16 + 4 * g;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (!MASKED || c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+            }
+            stage[r] = v;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                lds[buf * G::BUF + g * G::HA + (p / N + 1) * G::H + (p % N + 1)] = stage[r];
+            }
+        }
+    };
+
+    f4 acc[COW][PPW];
+#pragma unroll
+    for (int c = 0; c < COW; ++c)
+#pragma unroll
+        for (int j = 0; j < PPW; ++j) acc[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    load(0);
+    __syncthreads();   // the zero fill is complete before any interior store
+    store(0);
+    __syncthreads();
+
+    // The (tap, column group) steps of a chunk run as one unrolled stream:
+    // the B operand of step i + kRing is read from LDS while step i's MFMAs
+    // run, and each tap's A fragments are fetched from global memory one tap
+    // ahead, so neither read's latency stalls the matrix pipe. The sched
+    // group hints keep that interleave (a step's MFMAs, then the read kRing
+    // steps ahead) and pin each A fetch to the start of the tap before the
+    // one that uses it (left free, the scheduler sinks it next to its use
+    // to save four registers, and every tap then waits a full round trip).
+    constexpr int kRing = 4;
+    constexpr int STEPS = 9 * PPW;
+    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
+    auto loadA = [&](int q, int t, f4 (&a)[COW]) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
+    };
+    f4 aCur[COW], aNext[COW];
+    loadA(0, 0, aCur);
+    for (int q = 0; q < nq; ++q) {
+        // The last chunk fetches itself again in place of a next one (never
+        // stored), which keeps the step stream free of branches.
+        const int qn = q + 1 < nq ? q + 1 : q;
+        const f4* buf = lds + (q & 1) * G::BUF;
+        f4 ring[kRing];
+#pragma unroll
+        for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = buf[rofs[i % PPW] + tapOffset(i / PPW)];
+        __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);   // the ring's first reads
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+            const int t = i / PPW, pg = i % PPW;
+            if (pg == 0) {
+                // The next tap's A fragments (tap 8: the next chunk's first),
+                // and at tap 0 after them the next chunk's board planes: the
+                // count of outstanding loads drains in issue order, so tap
+                // 1's wait for its fragments does not wait for the planes.
+                loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
+                __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);   // issued here, a tap ahead
+                if (t == 0) load(qn);
+            }
+            const f4 bv = ring[i % kRing];
+            if (i + kRing < STEPS)
+                ring[i % kRing] = buf[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int c = 0; c < COW; ++c)
+                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
+            if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
+            if (pg == PPW - 1) {
+#pragma unroll
+                for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
+            }
+        }
+        if (q + 1 < nq) store((q + 1) & 1);
+        __syncthreads();
+    }
+
+    // The residual input may be the output buffer itself (the block's
+    // second convolution writes over its input), so the compiler cannot
+    // move a residual read above an earlier store. All of a lane's residual
+    // values are read first, in one batch, then combined and stored.
+    const float* skipb = skip ? skip + (size_t)b * cout * G::A : nullptr;
+    float* yb = y + (size_t)b * cout * G::A;
+    float sc[COW][4], sh[COW][4];
+#pragma unroll
+    for (int c = 0; c < COW; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
+            sc[c][r] = scale[co];
+            sh[c][r] = shift[co];
+        }
+    f4 res[COW][PPW];
+    if (skipb) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c)
+#pragma unroll
+            for (int j = 0; j < PPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    // Lanes past the board or past cout read a valid cell;
+                    // their values are never stored.
+                    const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
+                    const int p = min((pg0 + j) * 16 + n16, G::A - 1);
+                    res[c][j][r] = skipb[(size_t)co * G::A + p];
+                }
+    }
+#pragma unroll
+    for (int c = 0; c < COW; ++c) {
+        const int coBase = (cb0 + c) * 16 + 4 * k;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int co = coBase + r;
+            if (co >= cout) continue;
+#pragma unroll
+            for (int j = 0; j < PPW; ++j) {
+                const int p = (pg0 + j) * 16 + n16;
+                if (p < G::A)
+                    yb[(size_t)co * G::A + p] =
+                        epilogue(acc[c][j][r], sc[c][r], sh[c][r], skipb != nullptr, res[c][j][r], relu != 0);
+            }
+        }
+    }
+}
+
+// The residual tower's convolutions (cin = filters, a multiple of 16) and
+// the stem's (cin = 2H+2 input planes) are separate kernels, so profiles
+// tell them apart. Two waves per SIMD are asked for where the whole
+// workgroup shape allows it (one 16-channel block per wave).
+#define AZH_CONV_KERNEL(NAME, MASKED)                                                                      \
+    template <int N, int COW, int WCO, int WPG, int PPW>                                                  \
+    __global__ __launch_bounds__(WCO* WPG * 64)                                                          \
+        __attribute__((amdgpu_waves_per_eu(COW == 1 && WCO * WPG >= 4 ? 2 : 1,                           \
+                                           COW == 1 && WCO * WPG >= 4 ? 2 : 1))) void                    \
+        NAME(const float* __restrict__ x, const f4* __restrict__ wp, const float* __restrict__ scale,      \
+             const float* __restrict__ shift, const float* skip, float* y, int cin, int cout, int nq,      \
+             int coTiles, int pixTiles, int relu) {                                                        \
+        conv3x3Body<N, COW, WCO, WPG, PPW, MASKED>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,   \
+                                                   pixTiles, relu);                                        \
+    }
+AZH_CONV_KERNEL(conv3x3Tower, false)
+AZH_CONV_KERNEL(conv3x3Stem, true)
+#undef AZH_CONV_KERNEL
+
+} // namespace
+
+template <int N, int COW, int WCO, int WPG, int PPW>
+hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
+                       float* y, int B, int cin, int cout, bool relu, hipStream_t stream) {
+    constexpr int NPG = Geo<N>::NPG;
+    constexpr int pgPerWave = PPW == 0 ? NPG : PPW;
+    const int coTiles = ceilDiv(cout, 16 * COW * WCO);
+    const int pixTiles = ceilDiv(NPG, WPG * pgPerWave);
+    const int nq = ceilDiv(cin, kChunk);
+    const dim3 grid(B * coTiles * pixTiles), block(WCO * WPG * 64);
+    if (cin % kChunk == 0)
+        hipLaunchKernelGGL((conv3x3Tower<N, COW, WCO, WPG, PPW>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles, pixTiles,
+                           relu ? 1 : 0);
+    else
+        hipLaunchKernelGGL((conv3x3Stem<N, COW, WCO, WPG, PPW>), grid, block, 0, stream, x,
+                           reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles, pixTiles,
+                           relu ? 1 : 0);
+    return hipGetLastError();
+}
+
+} // namespace azh

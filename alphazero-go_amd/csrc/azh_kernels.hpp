@@ -48,6 +48,22 @@ struct ConvTiling {
     int coTile() const { return 16 * coPerWave * wavesCo; }
 };
 ConvTiling chooseConvTiling(int cout, int B, int boardSize);
+inline constexpr bool operator==(const ConvTiling& a, const ConvTiling& b) {
+    return a.coPerWave == b.coPerWave && a.wavesCo == b.wavesCo && a.wavesPg == b.wavesPg &&
+           a.pgPerWave == b.pgPerWave;
+}
+
+// The workgroup shapes the convolution is built for, in the order a probe
+// indexes them. Each is compiled for every supported board size.
+constexpr ConvTiling kConvTilings[] = {{2, 2, 2, 12}, {1, 4, 1, 0}, {1, 2, 1, 0}, {1, 1, 1, 0}, {1, 8, 1, 0},
+                                       {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1}};
+constexpr int kConvTilingCount = sizeof kConvTilings / sizeof kConvTilings[0];
+
+// One (board size, workgroup shape) instance of the convolution; defined in
+// azh_conv.hpp and instantiated by azh_conv_inst.hip, one object per shape.
+template <int N, int COW, int WCO, int WPG, int PPW>
+hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
+                       float* y, int B, int cin, int cout, bool relu, hipStream_t stream);
 
 // y[b][co][p] = relu?( (scale[co] * conv(x)[b][co][p] + shift[co]) (+ skip[b][co][p]) )
 // with each multiply and add rounded separately (BatchNorm2d::forwardInfer,
@@ -58,6 +74,14 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
                          const float* skip, float* y, int B, int n, int cin, int cout, bool relu, ConvTiling tiling,
                          hipStream_t stream);
 bool conv3x3Supported(int boardSize);
+
+// y = relu?(scale * acc + shift (+ skip)), each operation rounded on its own.
+__device__ inline float epilogue(float acc, float s, float h, bool addSkip, float skipv, bool relu) {
+    float v = __fadd_rn(__fmul_rn(s, acc), h);
+    if (addSkip) v = __fadd_rn(v, skipv);
+    if (relu) v = v > 0.0f ? v : 0.0f;   // -0 and NaN become +0 (reluForward)
+    return v;
+}
 
 // The heads (src/network.cpp:274-308), two kernels: the 1x1 convs F -> 2
 // (policy) and F -> 1 (value) with BN and ReLU, one position per workgroup,

@@ -31,6 +31,9 @@
 #ifndef AZH_KERNEL_HASH
 #define AZH_KERNEL_HASH "unhashed"
 #endif
+#ifndef AZH_CONV_HASH
+#define AZH_CONV_HASH "unhashed"
+#endif
 
 namespace {
 
@@ -77,9 +80,8 @@ constexpr size_t kMemoryMargin = size_t(512) << 20;
 constexpr int kPollFirstUs = 50, kPollLastUs = 200;
 constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
 // The workgroup shapes a probe may force (include/azgo_hip.h lists them).
-const azh::ConvTiling kTilings[] = {{2, 4, 1, 0}, {1, 4, 1, 0},  {1, 2, 1, 0}, {1, 1, 1, 0}, {1, 8, 1, 0},
-                                    {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1}};
-constexpr int kTilingCount = sizeof kTilings / sizeof kTilings[0];
+const azh::ConvTiling* const kTilings = azh::kConvTilings;
+constexpr int kTilingCount = azh::kConvTilingCount;
 
 // ---------------------------------------------------------------- context
 
@@ -640,7 +642,7 @@ int azh_describe(char* out, size_t cap) {
             char rt[32];
             std::snprintf(rt, sizeof rt, "%d.%d.%d", c.runtime / 10000000, (c.runtime / 100000) % 100,
                           c.runtime % 100000);
-            d = c.name + " " + base + ", HIP runtime " + rt + ", kernels " + AZH_KERNEL_HASH;
+            d = c.name + " " + base + ", HIP runtime " + rt + ", kernels " + AZH_KERNEL_HASH + " (conv " + AZH_CONV_HASH + ")";
         }
         if (out && cap) std::snprintf(out, cap, "%s", d.c_str());
     });

@@ -146,7 +146,8 @@ def main():
     conv_flops = w.trunk_conv_flops(B)
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
     pass_tflops = w.flops_per_position() * B / (ms_per_step * 1e-3) / 1e12
-    kernel_hash = azgo_hip.describe().rsplit("kernels ", 1)[-1]
+    # "..., kernels <all> (conv <conv>)": the traffic profile is keyed by the convolution's own hash.
+    kernel_hash = azgo_hip.describe().rsplit("(conv ", 1)[-1].rstrip(")")
     name = f"{n}x{n} {blocks}x{F} batch {B}"
     traffic = traffic_from_profile(name, kernel_hash)
 
