@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libazgo_hip.so")
 
 OK = 0
-ERR_ARGUMENT, ERR_UNAVAILABLE, ERR_MEMORY, ERR_TENSOR, ERR_HIP, ERR_STATE = -1, -2, -3, -4, -5, -6
+ERR_ARGUMENT, ERR_UNAVAILABLE, ERR_MEMORY, ERR_TENSOR, ERR_HIP, ERR_STATE, ERR_FORMAT = -1, -2, -3, -4, -5, -6, -7
 
 
 class NetCfg(C.Structure):
@@ -69,6 +69,11 @@ def load():
             "azh_check_memory": ([P(NetCfg), C.c_int, C.c_int, C.c_int], C.c_int),
             "azh_check_memory_bytes": ([C.c_double, C.c_int, C.c_int], C.c_int),
             "azh_create": ([P(NetCfg), P(Tensor), C.c_int, C.c_int, C.c_int, P(vp)], C.c_int),
+            "azh_tensor_count": ([P(NetCfg), P(C.c_int)], C.c_int),
+            "azh_tensor_info": ([P(NetCfg), C.c_int, C.c_char_p, C.c_size_t, P(C.c_size_t)], C.c_int),
+            "azh_checkpoint_config": ([C.c_char_p, P(NetCfg)], C.c_int),
+            "azh_checkpoint_read": ([C.c_char_p, P(NetCfg), f32, C.c_size_t, P(C.c_size_t)], C.c_int),
+            "azh_create_from_checkpoint": ([C.c_char_p, C.c_int, C.c_int, P(vp)], C.c_int),
             "azh_destroy": ([vp], None),
             "azh_slots": ([vp], C.c_int),
             "azh_max_batch": ([vp], C.c_int),
@@ -149,6 +154,42 @@ def check_memory(cfg, max_batch, hubs, slots_per_hub=2):
     _check(load().azh_check_memory(C.byref(cfg), max_batch, hubs, slots_per_hub))
 
 
+def tensor_spec(cfg):
+    """[(name, floats)] of the network's params() then buffers()."""
+    lib = load()
+    n = C.c_int()
+    _check(lib.azh_tensor_count(C.byref(cfg), C.byref(n)))
+    out = []
+    name = C.create_string_buffer(128)
+    size = C.c_size_t()
+    for i in range(n.value):
+        _check(lib.azh_tensor_info(C.byref(cfg), i, name, 128, C.byref(size)))
+        out.append((name.value.decode(), size.value))
+    return out
+
+
+def checkpoint_config(path):
+    """The NetCfg in an .azn checkpoint's header."""
+    cfg = NetCfg()
+    _check(load().azh_checkpoint_config(os.fsencode(path), C.byref(cfg)))
+    return cfg
+
+
+def checkpoint_read(path):
+    """(cfg, {name: float32 array}) from an .azn checkpoint, checked as
+    loadNetwork checks it."""
+    lib = load()
+    cfg, total = NetCfg(), C.c_size_t()
+    _check(lib.azh_checkpoint_read(os.fsencode(path), C.byref(cfg), None, 0, C.byref(total)))
+    values = np.empty(total.value, np.float32)
+    _check(lib.azh_checkpoint_read(os.fsencode(path), C.byref(cfg), _f(values), values.size, C.byref(total)))
+    tensors, off = {}, 0
+    for name, size in tensor_spec(cfg):
+        tensors[name] = values[off:off + size]
+        off += size
+    return cfg, tensors
+
+
 class Runner:
     """An azh_runner: the network's weights on the GPU, `slots` slots of up to
     max_batch positions. tensors: {name: float array} of the network's
@@ -166,6 +207,19 @@ class Runner:
         self.h = h
         self.max_batch = max_batch
         self._callbacks = {}
+
+    @classmethod
+    def from_checkpoint(cls, path, max_batch, slots=2):
+        """A runner straight from an .azn checkpoint (azh_create_from_checkpoint)."""
+        self = cls.__new__(cls)
+        self.lib = load()
+        self.cfg = checkpoint_config(path)
+        h = C.c_void_p()
+        _check(self.lib.azh_create_from_checkpoint(os.fsencode(path), max_batch, slots, C.byref(h)))
+        self.h = h
+        self.max_batch = max_batch
+        self._callbacks = {}
+        return self
 
     def close(self):
         if getattr(self, "h", None):

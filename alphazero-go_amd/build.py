@@ -64,7 +64,10 @@ def conv_tiling_count():
     return body.count("{")
 
 
-def build(verbose=False, jobs=None):
+def build(verbose=False, jobs=None, incremental=False):
+    """Compiles every unit and links libazgo_hip.so. incremental: skip units
+    whose object is newer than every source and header (a development aid;
+    the default rebuilds everything)."""
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
     defs = [f'-DAZH_KERNEL_HASH="{kernel_hash()}"', f'-DAZH_CONV_HASH="{conv_hash()}"']
@@ -73,9 +76,20 @@ def build(verbose=False, jobs=None):
         for t in range(conv_tiling_count()):
             units.append((CONV_INST, f"azh_conv_{n}_{t}.o", [f"-DAZH_CONV_N={n}", f"-DAZH_CONV_TILING={t}"]))
 
+    deps = [os.path.join(CSRC, f) for f in SOURCES + [CONV_INST] + HEADERS] + [os.path.abspath(__file__)]
+    newest = max(os.path.getmtime(f) for f in deps)
+
     def compile_one(unit):
         src, obj_name, extra = unit
         obj = os.path.join(build_dir, obj_name)
+        if incremental and os.path.exists(obj):
+            mine = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in HEADERS]
+            if src == CONV_INST:
+                mine = [os.path.join(CSRC, f) for f in [CONV_INST] + CONV_HEADERS] + [os.path.abspath(__file__)]
+            else:
+                mine += [os.path.abspath(__file__)]
+            if os.path.getmtime(obj) > max(os.path.getmtime(f) for f in mine):
+                return obj
         cmd = [HIPCC] + FLAGS + defs + extra + ["-c", os.path.join(CSRC, src), "-o", obj]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
@@ -112,5 +126,5 @@ def build_workload():
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, incremental="--incremental" in sys.argv))
     print(build_workload())

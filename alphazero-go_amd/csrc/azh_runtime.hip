@@ -3,7 +3,7 @@
 // params() and buffers()), weight packing and BN folding, per-slot device
 // workspaces with pinned staging and their own stream, the pass as one
 // hipGraph per batch size, the completion thread, timing entry points,
-// kernel probes and the test hooks.
+// kernel probes, the test hooks, and the .azn checkpoint reader.
 //
 // Compiled with -ffp-contract=off (host and device), so the host-side BN
 // fold rounds exactly as BatchNorm2d::forwardInfer does (src/layers.cpp:91-92).
@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstring>
 #include <deque>
+#include <fstream>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -283,6 +284,131 @@ std::map<std::string, const float*> checkTensors(const azh_netcfg& c, const azh_
         if (!given.count(x.name)) throw Error(AZH_ERR_TENSOR, "hip: tensor '" + x.name + "' missing");
     return given;
 }
+
+// ---------------------------------------------------------------- checkpoints (.azn)
+
+// The checkpoint format of saveNetwork / loadNetwork (src/checkpoint.cpp:84-124,
+// include/azgo/checkpoint.hpp:12-18), little-endian throughout: u32 magic
+// 0x4F475A41 ("AZGO"), u32 version (1; 2 adds the ownership flag), i32 board,
+// history, blocks, filters, value_hidden, in version 2 an i32 ownership flag
+// (0 or 1), u32 tensor count, then per tensor a u32 name length and the
+// name's bytes, a u64 float count and the floats (IEEE-754 bits), params()
+// then buffers() order. Failures read as loadNetwork's: the message names
+// the file and the problem, and running out of data is "truncated".
+constexpr uint32_t kAznMagic = 0x4F475A41;
+constexpr uint32_t kAznPlain = 1, kAznOwnership = 2;
+
+struct Truncated {};
+
+class AznReader {
+public:
+    explicit AznReader(const std::string& path) : path_(path), in_(path, std::ios::binary) {
+        if (!in_) throw Error(AZH_ERR_FORMAT, "cannot open checkpoint " + path);
+    }
+    [[noreturn]] void fail(const std::string& what) const { throw Error(AZH_ERR_FORMAT, path_ + ": " + what); }
+    void bytes(void* p, size_t n) {
+        in_.read(static_cast<char*>(p), static_cast<std::streamsize>(n));
+        if (static_cast<size_t>(in_.gcount()) != n) throw Truncated{};
+    }
+    uint32_t u32() {
+        unsigned char b[4];
+        bytes(b, 4);
+        return uint32_t(b[0]) | uint32_t(b[1]) << 8 | uint32_t(b[2]) << 16 | uint32_t(b[3]) << 24;
+    }
+    uint64_t u64() {
+        const uint64_t lo = u32();
+        return lo | uint64_t(u32()) << 32;
+    }
+    int32_t i32() { return static_cast<int32_t>(u32()); }
+    std::string str(size_t limit) {
+        const uint32_t len = u32();
+        if (len > limit) fail("tensor name of " + std::to_string(len) + " bytes");
+        std::string s(len, '\0');
+        if (len) bytes(&s[0], len);
+        return s;
+    }
+    void floats(float* out, size_t n) {
+        static_assert(sizeof(float) == 4, "IEEE-754 binary32");
+        unsigned char buf[4096];
+        while (n > 0) {
+            const size_t count = std::min(n, sizeof buf / 4);
+            bytes(buf, 4 * count);
+            for (size_t i = 0; i < count; ++i) {
+                const uint32_t bits = uint32_t(buf[4 * i]) | uint32_t(buf[4 * i + 1]) << 8 |
+                                      uint32_t(buf[4 * i + 2]) << 16 | uint32_t(buf[4 * i + 3]) << 24;
+                std::memcpy(out + i, &bits, 4);
+            }
+            out += count;
+            n -= count;
+        }
+    }
+    bool atEnd() { return in_.peek() == std::char_traits<char>::eof(); }
+
+    // The header (readHeader, src/checkpoint.cpp:37-60), with the shape
+    // ranges the reference's config accepts (kMaxBlocks 40, kMaxFilters 512,
+    // include/azgo/config.hpp:20-21).
+    azh_netcfg header() {
+        if (u32() != kAznMagic) fail("not an AZGO checkpoint");
+        const uint32_t version = u32();
+        if (version != kAznPlain && version != kAznOwnership) fail("unsupported version " + std::to_string(version));
+        azh_netcfg c{};
+        c.board = i32();
+        c.history = i32();
+        c.blocks = i32();
+        c.filters = i32();
+        c.value_hidden = i32();
+        c.ownership = 0;
+        if (version == kAznOwnership) {
+            const int32_t flag = i32();
+            if (flag != 0 && flag != 1) fail("invalid ownership flag in header");
+            c.ownership = flag;
+        }
+        if (c.board < 5 || c.board > 19 || c.history < 1 || c.history > 16 || c.blocks < 0 || c.blocks > 40 ||
+            c.filters < 1 || c.filters > 512 || c.value_hidden < 1 || c.value_hidden > 1024)
+            fail("invalid network shape in header");
+        return c;
+    }
+
+    // Every tensor, checked by position, name and size against the network
+    // the header describes (loadNetwork, src/checkpoint.cpp:102-124), into
+    // one array in file order.
+    std::vector<float> tensors(const std::vector<TensorSpec>& spec) {
+        size_t total = 0;
+        for (const TensorSpec& t : spec) total += t.size;
+        const uint32_t count = u32();
+        if (count != spec.size())
+            fail("has " + std::to_string(count) + " tensors but the network needs " + std::to_string(spec.size()));
+        std::vector<float> values(total);
+        size_t off = 0;
+        for (size_t i = 0; i < spec.size(); ++i) {
+            const std::string name = str(4096);
+            if (name != spec[i].name)
+                fail("tensor " + std::to_string(i) + " is '" + name + "' but expected '" + spec[i].name + "'");
+            const uint64_t size = u64();
+            if (size != spec[i].size)
+                fail("tensor '" + name + "' has " + std::to_string(size) + " values but expected " +
+                     std::to_string(spec[i].size));
+            floats(values.data() + off, spec[i].size);
+            off += spec[i].size;
+        }
+        if (!atEnd()) fail("unexpected data after the last tensor");
+        return values;
+    }
+
+    template <class Fn>
+    static auto read(const std::string& path, Fn&& fn) {
+        AznReader r(path);
+        try {
+            return fn(r);
+        } catch (const Truncated&) {
+            r.fail("truncated");
+        }
+    }
+
+private:
+    std::string path_;
+    std::ifstream in_;
+};
 
 // Packs, folds and uploads checked tensors into one device arena.
 void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*>& given, DeviceWeights& dw) {
@@ -619,6 +745,27 @@ struct azh_runner {
     }
 };
 
+// makeCudaRunner's steps (src/cuda/cuda_runner.cu:227-234): checks, memory,
+// upload, slots, the completion thread.
+void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
+                  azh_runner** out) {
+    if (!out) throw Error(AZH_ERR_ARGUMENT, "hip: no output handle");
+    *out = nullptr;
+    validate(cfg);
+    if (max_batch < 1) throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: maxBatch must be >= 1");
+    if (slots < 1 || slots > kMaxSlots)
+        throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: slots must be in [1, " + std::to_string(kMaxSlots) + "]");
+    const std::map<std::string, const float*> given = checkTensors(*cfg, tensors, count);
+    requireContext();
+    checkFits((double)runnerBytes(*cfg, max_batch, slots), max_batch, 1);
+    std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
+    uploadWeights(*cfg, given, r->weights);
+    for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
+    azh_runner* raw = r.get();
+    r->completion = std::thread([raw] { raw->completionLoop(); });
+    *out = r.release();
+}
+
 // ---------------------------------------------------------------- C ABI
 
 extern "C" {
@@ -679,22 +826,73 @@ int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs) {
 
 int azh_create(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
                azh_runner** out) {
+    return guarded([&] { createRunner(cfg, tensors, count, max_batch, slots, out); });
+}
+
+int azh_tensor_count(const azh_netcfg* cfg, int* count) {
     return guarded([&] {
-        if (!out) throw Error(AZH_ERR_ARGUMENT, "hip: no output handle");
-        *out = nullptr;
         validate(cfg);
-        if (max_batch < 1) throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: maxBatch must be >= 1");
-        if (slots < 1 || slots > kMaxSlots)
-            throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: slots must be in [1, " + std::to_string(kMaxSlots) + "]");
-        const std::map<std::string, const float*> given = checkTensors(*cfg, tensors, count);
-        requireContext();
-        checkFits((double)runnerBytes(*cfg, max_batch, slots), max_batch, 1);
-        std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
-        uploadWeights(*cfg, given, r->weights);
-        for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
-        azh_runner* raw = r.get();
-        r->completion = std::thread([raw] { raw->completionLoop(); });
-        *out = r.release();
+        if (!count) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        *count = (int)tensorSpec(*cfg).size();
+    });
+}
+
+int azh_tensor_info(const azh_netcfg* cfg, int i, char* name, size_t cap, size_t* size) {
+    return guarded([&] {
+        validate(cfg);
+        const std::vector<TensorSpec> spec = tensorSpec(*cfg);
+        if (i < 0 || i >= (int)spec.size()) throw Error(AZH_ERR_ARGUMENT, "hip: tensor index out of range");
+        if (name && cap) std::snprintf(name, cap, "%s", spec[i].name.c_str());
+        if (size) *size = spec[i].size;
+    });
+}
+
+int azh_checkpoint_config(const char* path, azh_netcfg* cfg) {
+    return guarded([&] {
+        if (!path || !cfg) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        *cfg = AznReader::read(path, [](AznReader& r) { return r.header(); });
+    });
+}
+
+int azh_checkpoint_read(const char* path, azh_netcfg* cfg, float* values, size_t cap, size_t* floats) {
+    return guarded([&] {
+        if (!path || !cfg || !floats) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        AznReader::read(path, [&](AznReader& r) {
+            const azh_netcfg c = r.header();
+            const std::vector<TensorSpec> spec = tensorSpec(c);
+            size_t total = 0;
+            for (const TensorSpec& t : spec) total += t.size;
+            *cfg = c;
+            *floats = total;
+            if (!values) return 0;
+            if (cap < total)
+                throw Error(AZH_ERR_ARGUMENT, "hip: checkpoint needs " + std::to_string(total) + " floats, got " +
+                                                  std::to_string(cap));
+            const std::vector<float> v = r.tensors(spec);
+            std::memcpy(values, v.data(), total * sizeof(float));
+            return 0;
+        });
+    });
+}
+
+int azh_create_from_checkpoint(const char* path, int max_batch, int slots, azh_runner** out) {
+    return guarded([&] {
+        if (!path || !out) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        *out = nullptr;
+        azh_netcfg c{};
+        std::vector<TensorSpec> spec;
+        const std::vector<float> values = AznReader::read(path, [&](AznReader& r) {
+            c = r.header();
+            spec = tensorSpec(c);
+            return r.tensors(spec);
+        });
+        std::vector<azh_tensor> tensors;
+        size_t off = 0;
+        for (const TensorSpec& t : spec) {
+            tensors.push_back({t.name.c_str(), values.data() + off, t.size});
+            off += t.size;
+        }
+        createRunner(&c, tensors.data(), (int)tensors.size(), max_batch, slots, out);
     });
 }
 

@@ -36,7 +36,8 @@ enum {
     AZH_ERR_MEMORY = -3,      /* std::runtime_error "... lower inference_batch" */
     AZH_ERR_TENSOR = -4,      /* std::logic_error naming a tensor (upload contract) */
     AZH_ERR_HIP = -5,         /* a HIP runtime error ("hip: ...") */
-    AZH_ERR_STATE = -6        /* a call the runner's state does not allow */
+    AZH_ERR_STATE = -6,       /* a call the runner's state does not allow */
+    AZH_ERR_FORMAT = -7       /* a checkpoint file loadNetwork would refuse (std::runtime_error naming the file) */
 };
 
 /* NetConfig (include/azgo/network.hpp:24-36). With ownership set the pass
@@ -113,6 +114,32 @@ int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs);
  * reads fail with AZH_ERR_TENSOR naming it. */
 int azh_create(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
                azh_runner** out);
+
+/* Network::params() then Network::buffers() for cfg (src/network.cpp:113-165):
+ * the number of tensors, and tensor i's name and size in floats. These are
+ * the tensors azh_create takes and the order a checkpoint stores them in. */
+int azh_tensor_count(const azh_netcfg* cfg, int* count);
+int azh_tensor_info(const azh_netcfg* cfg, int i, char* name, size_t cap, size_t* size);
+
+/* readCheckpointConfig (include/azgo/checkpoint.hpp:22; src/checkpoint.cpp:37-60,
+ * 126-128): the network shape in an .azn checkpoint's header. Failures are
+ * AZH_ERR_FORMAT with loadNetwork's message ("cannot open checkpoint <path>",
+ * "<path>: not an AZGO checkpoint", "<path>: unsupported version 3",
+ * "<path>: invalid network shape in header", "<path>: truncated", ...). */
+int azh_checkpoint_config(const char* path, azh_netcfg* cfg);
+
+/* loadNetwork (include/azgo/checkpoint.hpp:18-21; src/checkpoint.cpp:102-124)
+ * into caller memory: the header into cfg and *floats = the total size of
+ * every tensor; with values non-NULL (cap >= *floats) also every tensor,
+ * concatenated in params() then buffers() order (azh_tensor_info), each
+ * checked by position, name and size as loadNetwork checks it ("<path>:
+ * tensor 3 is 'x' but expected 'y'", "has 7 tensors but the network needs
+ * 9", "unexpected data after the last tensor", ...). */
+int azh_checkpoint_read(const char* path, azh_netcfg* cfg, float* values, size_t cap, size_t* floats);
+
+/* loadNetwork followed by makeCudaRunner: a runner straight from an .azn
+ * checkpoint (file errors as azh_checkpoint_read, then azh_create's). */
+int azh_create_from_checkpoint(const char* path, int max_batch, int slots, azh_runner** out);
 
 /* Waits for every pass in flight, then frees everything
  * (CudaBatchRunner::~CudaBatchRunner, src/cuda/cuda_runner.cu:64-71). */

@@ -417,18 +417,52 @@ def _ref():
         h.ref_im2col.argtypes = [f32, C.c_int, C.c_int, C.c_int, C.c_int, f32]
         h.ref_conv_forward.argtypes = [f32, C.c_int, C.c_int, C.c_int, f32, C.c_int, C.c_int, f32]
         h.ref_bn_infer.argtypes = [f32, f32, f32, f32, C.c_int, C.c_int, f32, f32]
+        h.ref_calibrate_bn.argtypes = [C.c_void_p, C.c_uint64, C.c_int]
+        h.ref_bn_calibration_positions.argtypes = [C.c_int, C.c_int, C.c_uint64, C.c_int, f32]
+        h.ref_save_network.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p, C.c_size_t]
+        h.ref_load_network.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        h.ref_load_network.restype = C.c_void_p
         _ref.h = h
     return _ref.h
+
+
+# The seed generation 0's batch-norm calibration uses: deriveSeed(seed = 1,
+# 0, kPhaseBatchNorm = 7) (src/trainer.cpp:559; include/azgo/run_state.hpp:120;
+# the config's default seed, include/azgo/config.hpp:39).
+PHASE_BATCH_NORM = 7
+
+
+def gen0_calibration_seed(seed=WEIGHT_SEED):
+    return derive_seed(seed, 0, PHASE_BATCH_NORM)
 
 
 class RefNetwork:
     """azgo::Network built by the reference's own code."""
 
-    def __init__(self, cfg, seed):
+    def __init__(self, cfg, seed, _ptr=None):
         self.cfg = cfg
         self.h = _ref()
-        self.ptr = self.h.ref_network_new(cfg.board, cfg.history, cfg.blocks, cfg.filters, cfg.value_hidden,
-                                          cfg.ownership, seed)
+        self.ptr = _ptr if _ptr is not None else self.h.ref_network_new(
+            cfg.board, cfg.history, cfg.blocks, cfg.filters, cfg.value_hidden, cfg.ownership, seed)
+
+    @classmethod
+    def load_file(cls, path, cfg):
+        """loadNetwork(path) (src/checkpoint.cpp:102-124); raises with its message."""
+        err = C.create_string_buffer(512)
+        ptr = _ref().ref_load_network(os.fsencode(path), err, 512)
+        if not ptr:
+            raise RuntimeError(err.value.decode())
+        return cls(cfg, 0, _ptr=ptr)
+
+    def save(self, path):
+        """saveNetwork (src/checkpoint.cpp:84-100)."""
+        err = C.create_string_buffer(512)
+        if self.h.ref_save_network(self.ptr, os.fsencode(path), err, 512):
+            raise RuntimeError(err.value.decode())
+
+    def calibrate_bn(self, seed, threads=8):
+        """calibrateBatchNorm (src/bn_calibration.cpp:33-45)."""
+        self.h.ref_calibrate_bn(self.ptr, seed, threads)
 
     def __del__(self):
         if getattr(self, "ptr", None):

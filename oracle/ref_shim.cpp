@@ -14,6 +14,8 @@
 #include <vector>
 
 #include "azgo/backend.hpp"
+#include "azgo/bn_calibration.hpp"
+#include "azgo/checkpoint.hpp"
 #include "azgo/encode.hpp"
 #include "azgo/layers.hpp"
 #include "azgo/network.hpp"
@@ -147,6 +149,38 @@ void ref_bn_infer(const float* gamma, const float* beta, const float* mean, cons
     std::memcpy(bn.runMean.data(), mean, C * sizeof(float));
     std::memcpy(bn.runVar.data(), var, C * sizeof(float));
     bn.forwardInfer(x, M, y);
+}
+
+// calibrateBatchNorm (src/bn_calibration.cpp:33-45): generation 0's
+// running statistics from one training-mode pass over the seeded positions.
+void ref_calibrate_bn(void* net, uint64_t seed, int threads) {
+    calibrateBatchNorm(*static_cast<Network*>(net), seed, threads);
+}
+
+// bnCalibrationPositions (src/bn_calibration.cpp:12-31): count x planes x area floats.
+void ref_bn_calibration_positions(int board, int history, uint64_t seed, int count, float* out) {
+    const std::vector<float> v = bnCalibrationPositions(board, history, seed, count);
+    std::memcpy(out, v.data(), v.size() * sizeof(float));
+}
+
+// saveNetwork / loadNetwork (src/checkpoint.cpp:84-128). Errors come back as
+// the message the reference throws, in err; the return is nonzero then.
+int ref_save_network(void* net, const char* path, char* err, size_t cap) {
+    try {
+        saveNetwork(*static_cast<Network*>(net), path);
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, cap, "%s", e.what());
+        return 1;
+    }
+}
+void* ref_load_network(const char* path, char* err, size_t cap) {
+    try {
+        return new Network(loadNetwork(path));
+    } catch (const std::exception& e) {
+        std::snprintf(err, cap, "%s", e.what());
+        return nullptr;
+    }
 }
 
 } // extern "C"

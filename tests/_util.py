@@ -1,4 +1,6 @@
 """Shared helpers of the tests (not collected: the name starts with _)."""
+import os
+
 import numpy as np
 
 import oracle as O
@@ -77,3 +79,25 @@ def parity_report(got_logits, got_values, ref_logits, ref_values, legal=None):
     if legal is not None:
         d["argmax_agree"] = float((O.legal_argmax(got_logits, legal) == O.legal_argmax(ref_logits, legal)).mean())
     return d
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def calibrated_network(tag, cfg=None):
+    """Generation 0 as the reference's trainer makes it: Network(cfg, 1)'s
+    weights (the oracle's init, pinned bitwise to the reference) with the
+    batch-norm running statistics the reference's calibrateBatchNorm wrote
+    (tests/golden/calibrated_bn.npz, key prefix `tag`)."""
+    if cfg is None:
+        cfg = O.WORKLOADS[int(tag)].cfg
+    net = O.init_network(cfg, synthetic_bn=False)
+    with np.load(os.path.join(GOLDEN, "calibrated_bn.npz")) as z:
+        found = 0
+        for name, t in net.tensors().items():
+            key = f"{tag}/{name}"
+            if key in z:
+                t[:] = z[key]
+                found += 1
+    assert found == 2 * (2 * cfg.blocks + 3 + (1 if cfg.ownership else 0)), found
+    return net

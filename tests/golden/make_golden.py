@@ -15,6 +15,17 @@ Vectors (data only, no reference source):
   infer_*.npz     Network::infer (naive backend) inputs and outputs: the
                   5x5 4x32 workload (seeded weights, synthetic BN statistics,
                   batch 8) and a 9x9 2x16 network with random BN and biases
+  calibrated_bn.npz  generation 0's batch-norm running statistics: every
+                  runMean/runVar of Network(cfg, 1) after calibrateBatchNorm
+                  (src/bn_calibration.cpp:33-45) with the trainer's seed
+                  deriveSeed(1, 0, 7) (src/trainer.cpp:559), for the five
+                  workloads' shapes and the 19x19 preset's value head of 256
+  gen0_*.azn      checkpoints written by saveNetwork (src/checkpoint.cpp:84-100):
+                  calibrated generation 0 of the 5x5 4x32 workload network
+                  (version 1) and of a 5x5 2x16 network with the ownership
+                  head (version 2)
+  gen0_infer.npz  Network::infer of those two checkpoints as loadNetwork
+                  reads them, on the 5x5 workload's batch of 8 positions
 """
 import hashlib
 import json
@@ -93,8 +104,46 @@ def main():
     tensors = {"t_" + k: v for k, v in net.tensors().items()}
     np.savez_compressed(os.path.join(HERE, "infer_9x9_random.npz"), input=inp, logits=logits, values=values,
                         **tensors)
+    calibrated()
     print("golden vectors written to", HERE)
 
 
+# Calibrated shapes: the workloads' networks (workload 4 is workload 3's)
+# and the 19x19 preset's value head (configs/19x19.cfg: value_hidden 256).
+CALIBRATED = {"1": O.WORKLOADS[1].cfg, "2": O.WORKLOADS[2].cfg, "3": O.WORKLOADS[3].cfg,
+              "5": O.WORKLOADS[5].cfg, "3v256": O.make_cfg(19, 10, 128, value_hidden=256)}
+
+
+def calibrated():
+    seed = O.gen0_calibration_seed()
+    out = {}
+    for tag, cfg in CALIBRATED.items():
+        ref = O.RefNetwork(cfg, 1)
+        ref.calibrate_bn(seed, threads=os.cpu_count() or 1)
+        for name, _, _, buf in ref.layout():
+            if buf:
+                out[f"{tag}/{name}"] = ref.get(name)
+        print("calibrated", tag, flush=True)
+    np.savez_compressed(os.path.join(HERE, "calibrated_bn.npz"), **out)
+
+    w = O.WORKLOADS[1]
+    inp, legal = O.workload_inputs(w, 8)
+    res = {"input": inp, "legal": legal}
+    for tag, cfg in (("4x32", w.cfg), ("2x16_own", O.make_cfg(5, 2, 16, ownership=1))):
+        ref = O.RefNetwork(cfg, 1)
+        ref.calibrate_bn(seed, threads=os.cpu_count() or 1)
+        path = os.path.join(HERE, f"gen0_5x5_{tag}.azn")
+        ref.save(path)
+        back = O.RefNetwork.load_file(path, cfg)
+        outs = back.infer(inp, ownership=bool(cfg.ownership))
+        res[f"{tag}/logits"], res[f"{tag}/values"] = outs[0], outs[1]
+        if cfg.ownership:
+            res[f"{tag}/ownership"] = outs[2]
+    np.savez_compressed(os.path.join(HERE, "gen0_infer.npz"), **res)
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["calibrated"]:
+        calibrated()
+    else:
+        main()
