@@ -42,6 +42,13 @@ class Tensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("data", C.POINTER(C.c_float)), ("size", C.c_size_t)]
 
 
+class Positions(C.Structure):
+    """azh_positions: a batch of positions as MCTS leaves hand them over."""
+    _fields_ = [("stones", C.POINTER(C.c_uint8)), ("plies", C.POINTER(C.c_int32)),
+                ("to_move", C.POINTER(C.c_uint8)), ("sym", C.POINTER(C.c_uint8)),
+                ("seen", C.POINTER(C.c_uint64)), ("seen_offsets", C.POINTER(C.c_int64))]
+
+
 DONE_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_char_p)
 
 
@@ -83,6 +90,9 @@ def load():
             "azh_begin": ([vp, C.c_int, C.c_int, DONE_FN, vp], C.c_int),
             "azh_infer": ([vp, f32, C.c_int, f32, f32, f32], C.c_int),
             "azh_softmax_legal": ([f32, u8, C.c_int, C.c_int, f32], C.c_int),
+            "azh_encode_planes": ([u8, P(C.c_int32), u8, u8, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_legal_moves": ([u8, C.c_int, u8, P(C.c_uint64), P(C.c_int64), C.c_int, u8], C.c_int),
+            "azh_evaluate_positions": ([vp, P(Positions), C.c_int, f32, f32, u8, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_enqueue": ([vp, C.c_int, C.c_int], C.c_int),
@@ -152,6 +162,51 @@ def memory_need(cfg, max_batch, slots):
 
 def check_memory(cfg, max_batch, hubs, slots_per_hub=2):
     _check(load().azh_check_memory(C.byref(cfg), max_batch, hubs, slots_per_hub))
+
+
+def _u8(a):
+    return None if a is None else a.ctypes.data_as(C.POINTER(C.c_uint8))
+
+
+def _seen_lists(seen, B):
+    """[list of uint64 hashes per position] -> (concatenated, offsets [B+1])."""
+    if seen is None:
+        seen = [()] * B
+    if len(seen) != B:
+        raise ValueError("one seen list per position")
+    offs = np.zeros(B + 1, np.int64)
+    for b, lst in enumerate(seen):
+        offs[b + 1] = offs[b] + len(lst)
+    flat = np.zeros(max(1, int(offs[-1])), np.uint64)
+    if offs[-1]:
+        flat[:offs[-1]] = np.concatenate([np.asarray(x, np.uint64).reshape(-1) for x in seen])
+    return flat, offs
+
+
+def encode_planes(stones, to_move, n, H, plies=None, sym=None):
+    """stones [B][H][n*n] bytes -> planes [B][2H+2][n*n] (azh_encode_planes)."""
+    stones = np.ascontiguousarray(stones, np.uint8)
+    B = stones.shape[0]
+    to_move = np.ascontiguousarray(to_move, np.uint8)
+    pl = None if plies is None else np.ascontiguousarray(plies, np.int32)
+    sy = None if sym is None else np.ascontiguousarray(sym, np.uint8)
+    out = np.empty((B, 2 * H + 2, n * n), np.float32)
+    _check(load().azh_encode_planes(_u8(stones), None if pl is None else pl.ctypes.data_as(C.POINTER(C.c_int32)),
+                                    _u8(to_move), _u8(sy), B, n, H, _f(out)))
+    return out
+
+
+def legal_moves(stones, to_move, n, seen=None):
+    """stones [B][n*n], to_move [B], seen: per position a list of hashes ->
+    legal [B][n*n+1] (azh_legal_moves)."""
+    stones = np.ascontiguousarray(stones, np.uint8).reshape(-1, n * n)
+    B = stones.shape[0]
+    to_move = np.ascontiguousarray(to_move, np.uint8)
+    flat, offs = _seen_lists(seen, B)
+    out = np.empty((B, n * n + 1), np.uint8)
+    _check(load().azh_legal_moves(_u8(stones), n, _u8(to_move), flat.ctypes.data_as(C.POINTER(C.c_uint64)),
+                                  offs.ctypes.data_as(C.POINTER(C.c_int64)), B, _u8(out)))
+    return out
 
 
 def tensor_spec(cfg):
@@ -248,6 +303,26 @@ class Runner:
         own = np.empty((B, self.cfg.board * self.cfg.board), np.float32) if ownership else None
         _check(self.lib.azh_infer(self.h, _f(inp), B, _f(logits), _f(values), _f(own) if ownership else None))
         return (logits, values, own) if ownership else (logits, values)
+
+    def evaluate_positions(self, stones, to_move, plies=None, sym=None, seen=None):
+        """The leaf evaluation on the GPU (azh_evaluate_positions): stones
+        [B][H][area] bytes -> (logits mapped back, priors, legal, values)."""
+        stones = np.ascontiguousarray(stones, np.uint8)
+        B = stones.shape[0]
+        to_move = np.ascontiguousarray(to_move, np.uint8)
+        pl = None if plies is None else np.ascontiguousarray(plies, np.int32)
+        sy = None if sym is None else np.ascontiguousarray(sym, np.uint8)
+        flat, offs = _seen_lists(seen, B)
+        pos = Positions(_u8(stones), None if pl is None else pl.ctypes.data_as(C.POINTER(C.c_int32)), _u8(to_move),
+                        _u8(sy), flat.ctypes.data_as(C.POINTER(C.c_uint64)), offs.ctypes.data_as(C.POINTER(C.c_int64)))
+        A1 = self.cfg.actions
+        logits = np.empty((B, A1), np.float32)
+        priors = np.empty((B, A1), np.float32)
+        legal = np.empty((B, A1), np.uint8)
+        values = np.empty(B, np.float32)
+        _check(self.lib.azh_evaluate_positions(self.h, C.byref(pos), B, _f(logits), _f(priors), _u8(legal),
+                                               _f(values)))
+        return logits, priors, legal, values
 
     def set_graphs(self, enabled):
         _check(self.lib.azh_set_graphs(self.h, int(enabled)))

@@ -1,8 +1,9 @@
 // The gfx950 kernels of the inference pass other than the 3x3 convolution
-// (azh_conv.hpp): the heads' 1x1 convolutions and Linear layers, the
-// legal-move softmax and the test hooks; plus the convolution's host side
-// (weight packing, the choice of workgroup shape, the dispatch to the
-// compiled instances).
+// (azh_conv.hpp): the heads' 1x1 convolutions and Linear layers and the
+// test hooks; plus the convolution's host side (weight packing, the choice
+// of workgroup shape, the dispatch to the compiled instances). The
+// legal-move softmax is azh_positions.hip's priors kernel without a
+// symmetry.
 //
 // MFMA operand layout (16x16x4 f32, wave64): A[i][k] comes from lane
 // i + 16k, B[k][j] from lane j + 16k, and lane j + 16g holds D[4g + r][j] in
@@ -158,33 +159,6 @@ __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ ac
     }
 }
 
-// ------------------------------------------------------------------ softmax over legal moves
-
-__global__ __launch_bounds__(256) void softmaxLegalKernel(const float* __restrict__ logits,
-                                                          const uint8_t* __restrict__ legal,
-                                                          float* __restrict__ priors, int B, int actions) {
-    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (pos >= B) return;   // a whole wave leaves together
-    const float* l = logits + (size_t)pos * actions;
-    const uint8_t* m = legal + (size_t)pos * actions;
-    float* o = priors + (size_t)pos * actions;
-    float mx = -INFINITY;
-    for (int a = lane; a < actions; a += 64)
-        if (m[a] && l[a] > mx) mx = l[a];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (mx == -INFINITY) {   // no legal action: nothing to normalise
-        for (int a = lane; a < actions; a += 64) o[a] = 0.0f;
-        return;
-    }
-    float sum = 0.0f;
-    for (int a = lane; a < actions; a += 64)
-        if (m[a]) sum += expf(l[a] - mx);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    for (int a = lane; a < actions; a += 64) o[a] = m[a] ? expf(l[a] - mx) / sum : 0.0f;
-}
-
 // ------------------------------------------------------------------ test hooks
 
 __global__ void spinKernel(unsigned long long ticks) {
@@ -293,10 +267,7 @@ size_t headFc1WTFloats(int n, int V) { return (size_t)headPad16(n * n) * headPad
 
 hipError_t launchSoftmaxLegal(const float* logits, const uint8_t* legal, float* priors, int B, int actions,
                               hipStream_t stream) {
-    if (B < 1) return hipSuccess;
-    hipLaunchKernelGGL(softmaxLegalKernel, dim3(ceilDiv(B, 4)), dim3(256), 0, stream, logits, legal, priors, B,
-                       actions);
-    return hipGetLastError();
+    return launchPriors(logits, legal, nullptr, nullptr, priors, B, actions, 0, stream);
 }
 
 hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream) {

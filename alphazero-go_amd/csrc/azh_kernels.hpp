@@ -111,6 +111,31 @@ hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, flo
 hipError_t launchSoftmaxLegal(const float* logits, const uint8_t* legal, float* priors, int B, int actions,
                               hipStream_t stream);
 
+// ---- the steps either side of the pass (azh_positions.hip)
+
+// encodePlanes (src/encode.cpp:14-43) for B positions: stones [B][H][n*n]
+// Color bytes (ply k = k moves ago, 0 = now), plies[b] of them present
+// (1..H; the rest are zero planes), toMove[b] 1 (Black) or 2 (White),
+// sym[b] 0..7 (NULL: identity) -> planes [B][2H+2][n*n].
+hipError_t launchEncodePlanes(const uint8_t* stones, const int* plies, const uint8_t* toMove, const uint8_t* sym,
+                              float* planes, int B, int n, int H, hipStream_t stream);
+
+// The legal actions of Mcts::expand (src/mcts.cpp:152-169) for B positions:
+// board b's stones at stones + b * stride (n*n Color bytes), toMove[b];
+// Board::isLegal plus positional superko against seen[seenOffsets[b] ..
+// seenOffsets[b+1]). legal [B][n*n+1] bytes, pass always 1. One workgroup
+// of 512 threads per position.
+hipError_t launchLegalMoves(const uint8_t* stones, size_t stride, const uint8_t* toMove, const uint64_t* seen,
+                            const long long* seenOffsets, uint8_t* legal, int B, int n, hipStream_t stream);
+
+// The priors of Mcts::evaluateLeaves + expand (src/mcts.cpp:136-146,
+// 170-183): the logits mapped back from symmetry sym[b] (NULL: identity;
+// action a reads logit transformAction(sym, a)), into mapped when not NULL,
+// then the softmax over the legal actions, into priors. actions = n*n + 1
+// when sym is given.
+hipError_t launchPriors(const float* logits, const uint8_t* legal, const uint8_t* sym, float* mapped, float* priors,
+                        int B, int actions, int n, hipStream_t stream);
+
 // Test hooks: holds the stream for about `nanoseconds` (a bounded wait on the
 // wall clock), and fills data[0..n) with value.
 hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream);

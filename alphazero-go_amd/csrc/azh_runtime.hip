@@ -499,6 +499,64 @@ size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
     return (size_t)slots * slotFloats(Shape(c), maxBatch) * sizeof(float) + weightFloats(c) * sizeof(float);
 }
 
+// A device allocation released on scope exit (the synchronous kernel entry points).
+struct DeviceBuffer {
+    void* p = nullptr;
+    explicit DeviceBuffer(size_t bytes) {
+        if (bytes) check(hipMalloc(&p, bytes), "hipMalloc");
+    }
+    ~DeviceBuffer() {
+        if (p) (void)hipFree(p);
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+// A device allocation that grows to the largest size asked of it.
+struct GrowingBuffer {
+    void* p = nullptr;
+    size_t cap = 0;
+    void* reserve(size_t bytes) {
+        if (bytes > cap) {
+            if (p) (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+            check(hipMalloc(&p, bytes), "hipMalloc");
+            cap = bytes;
+        }
+        return p;
+    }
+    ~GrowingBuffer() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+// The inputs a batch of positions brings (azh_positions), checked on the
+// host before anything reaches the GPU: every index the kernels form from
+// them then stays inside its array.
+void checkPositions(const uint8_t* stones, size_t stoneBytes, const int32_t* plies, const uint8_t* toMove,
+                    const uint8_t* sym, const int64_t* seenOffsets, const uint64_t* seen, int B, int H) {
+    if (!stones || !toMove || !seenOffsets) throw Error(AZH_ERR_ARGUMENT, "hip: positions need stones, to_move and seen_offsets");
+    for (size_t i = 0; i < stoneBytes; ++i)
+        if (stones[i] > 2) throw Error(AZH_ERR_ARGUMENT, "hip: a stone byte is not Empty (0), Black (1) or White (2)");
+    for (int b = 0; b < B; ++b) {
+        if (toMove[b] != 1 && toMove[b] != 2)
+            throw Error(AZH_ERR_ARGUMENT, "hip: position " + std::to_string(b) + " has no side to move (1 or 2)");
+        if (plies && (plies[b] < 1 || plies[b] > H))
+            throw Error(AZH_ERR_ARGUMENT, "hip: position " + std::to_string(b) + " has " + std::to_string(plies[b]) +
+                                              " plies of history, outside [1, " + std::to_string(H) + "]");
+        if (sym && sym[b] > 7) throw Error(AZH_ERR_ARGUMENT, "hip: symmetry outside [0, 8)");
+    }
+    if (seenOffsets[0] < 0) throw Error(AZH_ERR_ARGUMENT, "hip: seen_offsets[0] is negative");
+    for (int b = 0; b < B; ++b)
+        if (seenOffsets[b + 1] < seenOffsets[b]) throw Error(AZH_ERR_ARGUMENT, "hip: seen_offsets decrease");
+    if (seenOffsets[B] > 0 && !seen) throw Error(AZH_ERR_ARGUMENT, "hip: seen hashes missing");
+}
+
 struct Slot {
     hipStream_t stream = nullptr;
     hipEvent_t event = nullptr;
@@ -508,6 +566,11 @@ struct Slot {
     float *hIn = nullptr, *hLogits = nullptr, *hValues = nullptr;
     std::map<int, hipGraphExec_t> graphs;
     bool busy = false;
+    // The positions path (azh_evaluate_positions), allocated on first use:
+    // stones [maxBatch][H][A], plies, side to move, symmetry, superko list
+    // offsets, legal [maxBatch][A+1], mapped logits and priors, and the
+    // concatenated superko hashes (grown as needed).
+    GrowingBuffer posBytes, posSeen;
 
     Slot(const Shape& s, int maxBatch) {
         const size_t B = maxBatch;
@@ -988,6 +1051,122 @@ int azh_softmax_legal(const float* logits, const uint8_t* legal, int B, int acti
         check(hipMemcpy(dm, legal, n, hipMemcpyHostToDevice), "hipMemcpy");
         check(azh::launchSoftmaxLegal(dl, dm, dp, B, actions, nullptr), "softmax");
         check(hipMemcpy(priors, dp, n * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+int azh_encode_planes(const uint8_t* stones, const int32_t* plies, const uint8_t* to_move, const uint8_t* sym, int B,
+                      int n, int H, float* planes) {
+    return guarded([&] {
+        if (B < 0 || n < 5 || n > 19 || H < 1 || H > 16 || (B > 0 && !planes))
+            throw Error(AZH_ERR_ARGUMENT, "hip: encode needs n in [5, 19], H in [1, 16] and its arrays");
+        if (B == 0) return;
+        if (!stones || !to_move) throw Error(AZH_ERR_ARGUMENT, "hip: encode needs stones and to_move");
+        const int64_t zero[2] = {0, 0};
+        const size_t A = (size_t)n * n, stoneBytes = (size_t)B * H * A;
+        for (int b = 0; b < B; ++b)   // seen lists do not apply: check the rest one position at a time
+            checkPositions(stones + b * H * A, H * A, plies ? plies + b : nullptr, to_move ? to_move + b : nullptr,
+                           sym ? sym + b : nullptr, zero, nullptr, 1, H);
+        requireContext();
+        const size_t P = 2 * (size_t)H + 2;
+        DeviceBuffer dS(stoneBytes), dPl((size_t)B * sizeof(int)), dT(B), dSym(sym ? B : 0),
+            dOut((size_t)B * P * A * sizeof(float));
+        std::vector<int> pl(B, H);
+        if (plies) std::copy(plies, plies + B, pl.begin());
+        check(hipMemcpy(dS.p, stones, stoneBytes, hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dPl.p, pl.data(), (size_t)B * sizeof(int), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dT.p, to_move, B, hipMemcpyHostToDevice), "hipMemcpy");
+        if (sym) check(hipMemcpy(dSym.p, sym, B, hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchEncodePlanes(dS.as<uint8_t>(), dPl.as<int>(), dT.as<uint8_t>(), sym ? dSym.as<uint8_t>() : nullptr,
+                                      dOut.as<float>(), B, n, H, nullptr),
+              "encode");
+        check(hipMemcpy(planes, dOut.p, (size_t)B * P * A * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+int azh_legal_moves(const uint8_t* stones, int n, const uint8_t* to_move, const uint64_t* seen,
+                    const int64_t* seen_offsets, int B, uint8_t* legal) {
+    return guarded([&] {
+        if (B < 0 || n < 5 || n > 19 || (B > 0 && !legal))
+            throw Error(AZH_ERR_ARGUMENT, "hip: legal moves need n in [5, 19] and their arrays");
+        if (B == 0) return;
+        const size_t A = (size_t)n * n;
+        checkPositions(stones, (size_t)B * A, nullptr, to_move, nullptr, seen_offsets, seen, B, 1);
+        requireContext();
+        const size_t nSeen = (size_t)seen_offsets[B];
+        DeviceBuffer dS((size_t)B * A), dT(B), dSeen(nSeen * sizeof(uint64_t)), dOff((size_t)(B + 1) * sizeof(int64_t)),
+            dL((size_t)B * (A + 1));
+        check(hipMemcpy(dS.p, stones, (size_t)B * A, hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dT.p, to_move, B, hipMemcpyHostToDevice), "hipMemcpy");
+        if (nSeen) check(hipMemcpy(dSeen.p, seen, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dOff.p, seen_offsets, (size_t)(B + 1) * sizeof(int64_t), hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchLegalMoves(dS.as<uint8_t>(), A, dT.as<uint8_t>(), dSeen.as<uint64_t>(), dOff.as<long long>(),
+                                    dL.as<uint8_t>(), B, n, nullptr),
+              "legal moves");
+        check(hipMemcpy(legal, dL.p, (size_t)B * (A + 1), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float* logits, float* priors,
+                           uint8_t* legal, float* values) {
+    return guarded([&] {
+        if (!r || !pos || !priors || !legal || !values)
+            throw Error(AZH_ERR_ARGUMENT, "hip: evaluate_positions needs its arrays");
+        r->checkBatch(B);
+        const Shape& sh = r->shape;
+        const size_t A = sh.A, A1 = sh.A1, H = sh.H, M = r->maxBatch;
+        checkPositions(pos->stones, (size_t)B * H * A, pos->plies, pos->to_move, pos->sym, pos->seen_offsets,
+                       pos->seen, B, sh.H);
+        Slot& s = r->idleSlot(0);
+        // One allocation for the batch-sized parts, at the runner's maxBatch.
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t o = off;
+            off += (bytes + 255) / 256 * 256;
+            return o;
+        };
+        const size_t oStones = take(M * H * A), oPlies = take(M * sizeof(int)), oTurn = take(M), oSym = take(M),
+                     oOff = take((M + 1) * sizeof(int64_t)), oLegal = take(M * A1),
+                     oMapped = take(M * A1 * sizeof(float)), oPriors = take(M * A1 * sizeof(float));
+        uint8_t* base = static_cast<uint8_t*>(s.posBytes.reserve(off));
+        const size_t nSeen = (size_t)pos->seen_offsets[B];
+        uint64_t* dSeen = static_cast<uint64_t*>(s.posSeen.reserve(std::max<size_t>(nSeen, 1) * sizeof(uint64_t)));
+        std::vector<int> pl(B, sh.H);
+        if (pos->plies) std::copy(pos->plies, pos->plies + B, pl.begin());
+        std::vector<uint8_t> sy(B, 0);
+        if (pos->sym) std::copy(pos->sym, pos->sym + B, sy.begin());
+        auto up = [&](size_t o, const void* src, size_t bytes) {
+            check(hipMemcpyAsync(base + o, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(positions)");
+        };
+        up(oStones, pos->stones, (size_t)B * H * A);
+        up(oPlies, pl.data(), (size_t)B * sizeof(int));
+        up(oTurn, pos->to_move, B);
+        up(oSym, sy.data(), B);
+        up(oOff, pos->seen_offsets, (size_t)(B + 1) * sizeof(int64_t));
+        if (nSeen)
+            check(hipMemcpyAsync(dSeen, pos->seen, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice, s.stream),
+                  "hipMemcpyAsync(seen)");
+        const uint8_t* dStones = base + oStones;
+        const uint8_t* dTurn = base + oTurn;
+        const uint8_t* dSym = base + oSym;
+        uint8_t* dLegal = base + oLegal;
+        float* dMapped = reinterpret_cast<float*>(base + oMapped);
+        float* dPriors = reinterpret_cast<float*>(base + oPriors);
+        check(azh::launchEncodePlanes(dStones, reinterpret_cast<const int*>(base + oPlies), dTurn, dSym, s.dIn, B, sh.n,
+                                      sh.H, s.stream),
+              "encode");
+        r->enqueuePass(s, B);
+        check(azh::launchLegalMoves(dStones, H * A, dTurn, dSeen, reinterpret_cast<const long long*>(base + oOff),
+                                    dLegal, B, sh.n, s.stream),
+              "legal moves");
+        check(azh::launchPriors(s.dLogits, dLegal, dSym, dMapped, dPriors, B, (int)A1, sh.n, s.stream), "priors");
+        auto down = [&](void* dst, const void* src, size_t bytes) {
+            check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(outputs)");
+        };
+        down(priors, dPriors, (size_t)B * A1 * sizeof(float));
+        down(legal, dLegal, (size_t)B * A1);
+        down(values, s.dValues, (size_t)B * sizeof(float));
+        if (logits) down(logits, dMapped, (size_t)B * A1 * sizeof(float));
+        check(hipStreamSynchronize(s.stream), "GPU inference failed");
     });
 }
 

@@ -178,6 +178,52 @@ int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* va
  * Host arrays [B][actions]; runs on its own stream and waits. */
 int azh_softmax_legal(const float* logits, const uint8_t* legal, int B, int actions, float* priors);
 
+/* ---------------------------------------------------------------- the steps either side of the pass */
+
+/* encodePlanes (src/encode.cpp:14-43; include/azgo/encode.hpp:20-27) on the
+ * GPU for B positions: stones [B][H][n*n] Color bytes (0 Empty, 1 Black,
+ * 2 White; ply k = the position k moves ago, k = 0 the current one, as
+ * Mcts::evaluateLeaves gathers them, src/mcts.cpp:119-132), plies[b] of them
+ * present (1..H; NULL: all H), to_move[b] (1 Black, 2 White: "own" stones
+ * are the side to move's), sym[b] (0..7, transformPoint; NULL: identity) ->
+ * planes [B][2H+2][n*n]. Host arrays; waits. */
+int azh_encode_planes(const uint8_t* stones, const int32_t* plies, const uint8_t* to_move, const uint8_t* sym, int B,
+                      int n, int H, float* planes);
+
+/* The legal actions Mcts::expand builds for a node (src/mcts.cpp:152-169) on
+ * the GPU for B positions: Board::isLegal (src/board.cpp:131-150: empty,
+ * not suicide) and positional superko: the stones after the move
+ * (Board::hashAfter, src/board.cpp:176-190) may not hash to any of
+ * seen[seen_offsets[b] .. seen_offsets[b+1]) (the game's positions and the
+ * node's path, Zobrist hashes as Board::hash). stones [B][n*n], to_move[B]
+ * (1 Black, 2 White) -> legal [B][n*n+1] (1 legal, 0 not; pass always 1).
+ * Host arrays; waits. */
+int azh_legal_moves(const uint8_t* stones, int n, const uint8_t* to_move, const uint64_t* seen,
+                    const int64_t* seen_offsets, int B, uint8_t* legal);
+
+/* A batch of positions as MCTS leaves hand them over: the arrays of
+ * azh_encode_planes (stones [B][H][n*n] with ply 0 the board the legal
+ * moves are for) and of azh_legal_moves (the superko lists). */
+typedef struct azh_positions {
+    const uint8_t* stones;       /* [B][H][n*n] */
+    const int32_t* plies;        /* [B], 1..H; NULL: all H */
+    const uint8_t* to_move;      /* [B], 1 Black, 2 White */
+    const uint8_t* sym;          /* [B], 0..7; NULL: identity */
+    const uint64_t* seen;        /* every position's superko hashes, concatenated */
+    const int64_t* seen_offsets; /* [B+1] */
+} azh_positions;
+
+/* The leaf evaluation of Mcts::evaluateLeaves and the priors of
+ * Mcts::expand (src/mcts.cpp:113-183) as one synchronous GPU call on slot
+ * 0: positions encoded on the GPU, the pass, the legal actions, the logits
+ * mapped back from each position's symmetry (action a <- logit
+ * transformAction(sym, a), src/mcts.cpp:136-146), the softmax over the legal
+ * actions. Outputs [B][n*n+1]: logits (mapped back; may be NULL), priors
+ * (0 where illegal), legal; values [B]. The host copies carry stone bytes,
+ * not planes: 2H+2 floats per point become H bytes. */
+int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float* logits, float* priors,
+                           uint8_t* legal, float* values);
+
 /* Whether passes replay a captured hipGraph per batch size (default 1), or
  * launch their kernels one by one. */
 int azh_set_graphs(azh_runner* r, int enabled);

@@ -30,6 +30,11 @@
  *   double pass  brute force on tiny inputs; closed-form hand networks.
  *   softmax      sums to 1 over legal moves, zero elsewhere; closed form on
  *                hand logits.
+ *   rules        the legal-move positions of tests/test_board.cpp:109-146 and
+ *                the ko of tests/test_game.cpp:19-55, restated; whole random
+ *                games (every position's stones, hash and legal set) played
+ *                move for move identically by the reference's Game compiled
+ *                from source (tests/golden/games.npz).
  */
 #define _GNU_SOURCE
 #include <dlfcn.h>
@@ -392,6 +397,256 @@ void azo_encode_batch(int n, int H, int B, const uint8_t* stones, const uint8_t*
             legal[(size_t)i * (area + 1) + area] = 1;
         }
     }
+}
+
+/* ------------------------------------------------------------------ rules: legal moves and superko */
+
+/* The padded board of include/azgo/board.hpp:21-24: rows of 21 cells (a
+ * sentinel column each side of the largest board), cells Empty 0, Black 1,
+ * White 2, Off 3 outside the n x n area. */
+#define AZO_STRIDE 21
+#define AZO_CELLS (AZO_STRIDE * AZO_STRIDE)
+enum { AZO_EMPTY = 0, AZO_BLACK = 1, AZO_WHITE = 2, AZO_OFF = 3 };
+
+static uint64_t zkeys[AZO_CELLS][2];
+static pthread_once_t zonce = PTHREAD_ONCE_INIT;
+
+/* src/board.cpp:19-33: one key per (padded cell, colour), black then white
+ * for each cell in order, from one splitmix64 stream seeded 0x5EEDB0A4D5EEDB0A. */
+static void zinit(void) {
+    uint64_t x = 0x5EEDB0A4D5EEDB0AULL;
+    for (int c = 0; c < AZO_CELLS; ++c) {
+        zkeys[c][0] = azo_splitmix64(&x);
+        zkeys[c][1] = azo_splitmix64(&x);
+    }
+}
+
+uint64_t azo_zobrist_key(int padded, int color) {
+    pthread_once(&zonce, zinit);
+    return zkeys[padded][color == AZO_BLACK ? 0 : 1];
+}
+
+typedef struct {
+    int n, to_move;
+    uint8_t cell[AZO_CELLS];
+    uint64_t hash;
+} azo_board;
+
+static int padded(int n, int p) { return (p / n + 1) * AZO_STRIDE + (p % n + 1); }
+static int other(int c) { return c == AZO_BLACK ? AZO_WHITE : AZO_BLACK; }
+static const int kDirs[4] = {-AZO_STRIDE, -1, 1, AZO_STRIDE};
+
+/* Board(n) + setStone per point (src/board.cpp:44-52, 273-281): the hash is
+ * the XOR of the keys of every stone. */
+static void board_from(azo_board* b, int n, const uint8_t* stones, int to_move) {
+    b->n = n;
+    b->to_move = to_move;
+    b->hash = 0;
+    memset(b->cell, AZO_OFF, sizeof b->cell);
+    for (int p = 0; p < n * n; ++p) {
+        const int q = padded(n, p);
+        b->cell[q] = stones[p];
+        if (stones[p] == AZO_BLACK || stones[p] == AZO_WHITE) b->hash ^= azo_zobrist_key(q, stones[p]);
+    }
+}
+
+/* Board::countLiberties (src/board.cpp:68-94): flood fill over the group at
+ * padded cell p; each liberty counted once; stops once `limit` are found. */
+static int count_libs(const azo_board* b, int p, int limit) {
+    int stack[AZO_CELLS], top = 0, libs = 0;
+    uint8_t mark[AZO_CELLS];
+    memset(mark, 0, sizeof mark);
+    const int color = b->cell[p];
+    stack[top++] = p;
+    mark[p] = 1;
+    while (top > 0) {
+        const int q = stack[--top];
+        for (int d = 0; d < 4; ++d) {
+            const int r = q + kDirs[d];
+            if (mark[r]) continue;
+            if (b->cell[r] == AZO_EMPTY) {
+                mark[r] = 1;
+                if (++libs >= limit) return libs;
+            } else if (b->cell[r] == color) {
+                mark[r] = 1;
+                stack[top++] = r;
+            }
+        }
+    }
+    return libs;
+}
+
+/* Board::removeGroup (src/board.cpp:96-121). */
+static int remove_group(azo_board* b, int p) {
+    int stack[AZO_CELLS], top = 0, removed = 0;
+    const int color = b->cell[p];
+    stack[top++] = p;
+    b->cell[p] = AZO_EMPTY;
+    b->hash ^= azo_zobrist_key(p, color);
+    while (top > 0) {
+        const int q = stack[--top];
+        ++removed;
+        for (int d = 0; d < 4; ++d) {
+            const int r = q + kDirs[d];
+            if (b->cell[r] == color) {
+                b->cell[r] = AZO_EMPTY;
+                b->hash ^= azo_zobrist_key(r, color);
+                stack[top++] = r;
+            }
+        }
+    }
+    return removed;
+}
+
+/* Board::isLegal (src/board.cpp:131-150): pass always; else an empty point
+ * where the new stone gets a liberty from an empty neighbour, from capturing
+ * an opponent group whose last liberty it is, or from a friendly group with
+ * another liberty. Superko is not checked here. */
+static int is_legal(const azo_board* b, int action) {
+    const int area = b->n * b->n;
+    if (action == area) return 1;
+    if (action < 0 || action > area) return 0;
+    const int p = padded(b->n, action);
+    if (b->cell[p] != AZO_EMPTY) return 0;
+    const int me = b->to_move, them = other(me);
+    for (int d = 0; d < 4; ++d) {
+        const int q = p + kDirs[d];
+        const int c = b->cell[q];
+        if (c == AZO_EMPTY) return 1;
+        if (c == them && count_libs(b, q, 2) == 1) return 1;
+        if (c == me && count_libs(b, q, 2) >= 2) return 1;
+    }
+    return 0;
+}
+
+/* Board::play (src/board.cpp:152-174): places the stone, removes opponent
+ * groups left without liberties, passes the turn. Returns stones captured. */
+static int play(azo_board* b, int action) {
+    const int area = b->n * b->n;
+    if (action == area) {
+        b->to_move = other(b->to_move);
+        return 0;
+    }
+    const int p = padded(b->n, action);
+    const int me = b->to_move, them = other(me);
+    b->cell[p] = (uint8_t)me;
+    b->hash ^= azo_zobrist_key(p, me);
+    int captured = 0;
+    for (int d = 0; d < 4; ++d) {
+        const int q = p + kDirs[d];
+        if (b->cell[q] == them && count_libs(b, q, 1) == 0) captured += remove_group(b, q);
+    }
+    b->to_move = them;
+    return captured;
+}
+
+/* Board::hashAfter (src/board.cpp:176-190) for a legal action: the move is
+ * played on a copy only when an opponent group beside it has exactly one
+ * liberty; otherwise the hash gains the new stone's key alone (which
+ * differs from play() only where an opponent group beside the point already
+ * has no liberty, a position no game reaches). */
+static uint64_t hash_after(const azo_board* b, int action) {
+    if (action == b->n * b->n) return b->hash;
+    const int p = padded(b->n, action), them = other(b->to_move);
+    for (int d = 0; d < 4; ++d) {
+        const int q = p + kDirs[d];
+        if (b->cell[q] == them && count_libs(b, q, 2) == 1) {
+            azo_board next = *b;
+            play(&next, action);
+            return next.hash;
+        }
+    }
+    return b->hash ^ azo_zobrist_key(p, b->to_move);
+}
+
+static int seen_has(const uint64_t* seen, int nseen, uint64_t h) {
+    for (int i = 0; i < nseen; ++i)
+        if (seen[i] == h) return 1;
+    return 0;
+}
+
+/* The legal set Mcts::expand builds (src/mcts.cpp:152-169), and
+ * Game::isLegal for a game that is not over (src/game.cpp:19-29): pass, and
+ * every point Board::isLegal allows whose resulting stones are not among
+ * `seen` (positional superko). legal[0..n*n] = 1 / 0. */
+void azo_legal_moves(const uint8_t* stones, int n, int to_move, const uint64_t* seen, int nseen, uint8_t* legal) {
+    azo_board b;
+    board_from(&b, n, stones, to_move);
+    for (int a = 0; a < n * n; ++a)
+        legal[a] = (uint8_t)(is_legal(&b, a) && !seen_has(seen, nseen, hash_after(&b, a)));
+    legal[n * n] = 1;
+}
+
+/* Board::isLegal alone (no superko) for every action. */
+void azo_board_legal(const uint8_t* stones, int n, int to_move, uint8_t* legal) {
+    azo_board b;
+    board_from(&b, n, stones, to_move);
+    for (int a = 0; a <= n * n; ++a) legal[a] = (uint8_t)is_legal(&b, a);
+}
+
+uint64_t azo_board_hash(const uint8_t* stones, int n) {
+    azo_board b;
+    board_from(&b, n, stones, AZO_BLACK);
+    return b.hash;
+}
+
+/* Board::hashAfter for every action (0 where Board::isLegal refuses it). */
+void azo_hash_after(const uint8_t* stones, int n, int to_move, uint64_t* out) {
+    azo_board b;
+    board_from(&b, n, stones, to_move);
+    for (int a = 0; a <= n * n; ++a) out[a] = is_legal(&b, a) ? hash_after(&b, a) : 0;
+}
+
+/* Board::play on a copy: the stones after `action` (which must be legal). */
+int azo_play(const uint8_t* stones, int n, int to_move, int action, uint8_t* out) {
+    azo_board b;
+    board_from(&b, n, stones, to_move);
+    const int captured = play(&b, action);
+    for (int p = 0; p < n * n; ++p) out[p] = b.cell[padded(n, p)];
+    return captured;
+}
+
+/* A random game as bnCalibrationPositions plays them (src/bn_calibration.cpp:19-28):
+ * from the empty board, Black first, each move a uniformly random legal
+ * point (Rng::below over Game::legalActions' points, ascending), a pass only
+ * when no point is legal; stops after `moves` moves or when the game ends
+ * (two passes, or 2 n^2 moves: src/game.cpp:51-53, 69-71). Records every
+ * position 0..played: stones [moves+1][n*n], side to move, Zobrist hash and
+ * the legal set (Game::isLegal: superko against every earlier position and
+ * the current one) [moves+1][n*n+1]. Returns the moves played. */
+int azo_random_game(int n, uint64_t seed, int moves, uint8_t* stones, uint8_t* to_move, uint64_t* hashes,
+                    uint8_t* legal) {
+    const int area = n * n, max_moves = 2 * area;
+    azo_rng rng;
+    azo_rng_init(&rng, seed);
+    azo_board b;
+    uint8_t* empty = calloc((size_t)area, 1);
+    board_from(&b, n, empty, AZO_BLACK);
+    free(empty);
+    uint64_t* seen = malloc(sizeof(uint64_t) * (size_t)(moves + 1));
+    int nseen = 0, passes = 0, ply = 0;
+    int* points = malloc(sizeof(int) * (size_t)area);
+    for (;;) {
+        for (int p = 0; p < area; ++p) stones[(size_t)ply * area + p] = b.cell[padded(n, p)];
+        to_move[ply] = (uint8_t)b.to_move;
+        hashes[ply] = b.hash;
+        if (!seen_has(seen, nseen, b.hash)) seen[nseen++] = b.hash;
+        uint8_t* lg = legal + (size_t)ply * (area + 1);
+        int count = 0;
+        for (int a = 0; a < area; ++a) {
+            lg[a] = (uint8_t)(is_legal(&b, a) && !seen_has(seen, nseen, hash_after(&b, a)));
+            if (lg[a]) points[count++] = a;
+        }
+        lg[area] = 1;
+        if (ply == moves || passes >= 2 || ply >= max_moves) break;
+        const int action = count > 0 ? points[azo_rng_below(&rng, count)] : area;
+        passes = action == area ? passes + 1 : 0;
+        play(&b, action);
+        ++ply;
+    }
+    free(points);
+    free(seen);
+    return ply;
 }
 
 /* ------------------------------------------------------------------ cblas */

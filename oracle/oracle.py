@@ -119,6 +119,16 @@ def _lib():
         h.azo_forward.argtypes = [P(Cfg), f32, f32, f32, C.c_int, C.c_int, f32, f32, f32]
         h.azo_forward_double.argtypes = [P(Cfg), f32, f32, f32, C.c_int, f32, f32, f32]
         h.azo_softmax_legal.argtypes = [f32, u8, C.c_int, C.c_int, f32]
+        u64p = P(C.c_uint64)
+        h.azo_zobrist_key.argtypes = [C.c_int, C.c_int]
+        h.azo_zobrist_key.restype = C.c_uint64
+        h.azo_legal_moves.argtypes = [u8, C.c_int, C.c_int, u64p, C.c_int, u8]
+        h.azo_board_legal.argtypes = [u8, C.c_int, C.c_int, u8]
+        h.azo_board_hash.argtypes = [u8, C.c_int]
+        h.azo_board_hash.restype = C.c_uint64
+        h.azo_hash_after.argtypes = [u8, C.c_int, C.c_int, u64p]
+        h.azo_play.argtypes = [u8, C.c_int, C.c_int, C.c_int, u8]
+        h.azo_random_game.argtypes = [C.c_int, C.c_uint64, C.c_int, u8, u8, u64p, u8]
         h.azo_time_workers.argtypes = [P(Cfg), f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                        P(C.c_double)]
         h.azo_time_workers.restype = C.c_double
@@ -355,6 +365,69 @@ def softmax_legal(logits, legal):
     return out
 
 
+# ------------------------------------------------------------------ rules (legal moves, superko)
+
+EMPTY, BLACK, WHITE = 0, 1, 2
+
+
+def _u64p(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint64))
+
+
+def zobrist_key(padded_cell, color):
+    return _lib().azo_zobrist_key(padded_cell, color)
+
+
+def board_hash(stones, n):
+    s = np.ascontiguousarray(stones, np.uint8)
+    return _lib().azo_board_hash(u8ptr(s), n)
+
+
+def legal_moves(stones, n, to_move, seen=()):
+    """Mcts::expand's legal set: Board::isLegal and no superko repeat of `seen`."""
+    s = np.ascontiguousarray(stones, np.uint8)
+    h = np.ascontiguousarray(np.asarray(seen, np.uint64).reshape(-1))
+    out = np.empty(n * n + 1, np.uint8)
+    _lib().azo_legal_moves(u8ptr(s), n, to_move, _u64p(h), h.size, u8ptr(out))
+    return out
+
+
+def board_legal(stones, n, to_move):
+    s = np.ascontiguousarray(stones, np.uint8)
+    out = np.empty(n * n + 1, np.uint8)
+    _lib().azo_board_legal(u8ptr(s), n, to_move, u8ptr(out))
+    return out
+
+
+def hash_after(stones, n, to_move):
+    s = np.ascontiguousarray(stones, np.uint8)
+    out = np.empty(n * n + 1, np.uint64)
+    _lib().azo_hash_after(u8ptr(s), n, to_move, _u64p(out))
+    return out
+
+
+def play(stones, n, to_move, action):
+    """(stones after the move, stones captured)."""
+    s = np.ascontiguousarray(stones, np.uint8)
+    out = np.empty(n * n, np.uint8)
+    captured = _lib().azo_play(u8ptr(s), n, to_move, action, u8ptr(out))
+    return out, captured
+
+
+def random_game(n, seed, moves, ref=False):
+    """Every position of a random game (bnCalibrationPositions' move choice):
+    (stones [k+1][n*n], to_move [k+1], hashes [k+1], legal [k+1][n*n+1]).
+    ref=True plays it with the reference's own Game (oracle/_ref)."""
+    area = n * n
+    stones = np.zeros((moves + 1, area), np.uint8)
+    to_move = np.zeros(moves + 1, np.uint8)
+    hashes = np.zeros(moves + 1, np.uint64)
+    legal = np.zeros((moves + 1, area + 1), np.uint8)
+    fn = _ref().ref_random_game if ref else _lib().azo_random_game
+    k = fn(n, seed, moves, u8ptr(stones), u8ptr(to_move), _u64p(hashes), u8ptr(legal))
+    return stones[:k + 1], to_move[:k + 1], hashes[:k + 1], legal[:k + 1]
+
+
 def time_workers(net: Net, inp, workers, calls, mode=BLAS, warm=True):
     """Positions/s of `workers` threads each running `calls` single-threaded
     passes over inp (after one warm-up pass when `warm`); returns (rate,
@@ -422,6 +495,12 @@ def _ref():
         h.ref_save_network.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p, C.c_size_t]
         h.ref_load_network.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
         h.ref_load_network.restype = C.c_void_p
+        u64p = P(C.c_uint64)
+        h.ref_random_game.argtypes = [C.c_int, C.c_uint64, C.c_int, u8, u8, u64p, u8]
+        h.ref_board_legal.argtypes = [u8, C.c_int, C.c_int, u8]
+        h.ref_hash_after.argtypes = [u8, C.c_int, C.c_int, u64p]
+        h.ref_board_hash.argtypes = [u8, C.c_int]
+        h.ref_board_hash.restype = C.c_uint64
         _ref.h = h
     return _ref.h
 

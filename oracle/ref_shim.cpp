@@ -17,6 +17,7 @@
 #include "azgo/bn_calibration.hpp"
 #include "azgo/checkpoint.hpp"
 #include "azgo/encode.hpp"
+#include "azgo/game.hpp"
 #include "azgo/layers.hpp"
 #include "azgo/network.hpp"
 #include "azgo/param_layout.hpp"
@@ -182,5 +183,48 @@ void* ref_load_network(const char* path, char* err, size_t cap) {
         return nullptr;
     }
 }
+
+// A random game played by the reference's Game with bnCalibrationPositions'
+// move choice (src/bn_calibration.cpp:19-28): each move legal[rng.below(points)]
+// over Game::legalActions (ascending, pass last), a pass only when no point
+// is legal. Records every position: stones, side to move, Board::hash, and
+// the legal set as Mcts::expand builds it at a root (src/mcts.cpp:152-169:
+// Board::isLegal and hashAfter not seen in the game). Returns moves played.
+int ref_random_game(int n, uint64_t seed, int moves, uint8_t* stones, uint8_t* toMove, uint64_t* hashes,
+                    uint8_t* legal) {
+    Game game(n, 0.0f, defaultMaxMoves(n));
+    Rng rng(seed);
+    const int area = n * n;
+    for (int ply = 0;; ++ply) {
+        const Board& b = game.board();
+        b.exportStones(stones + static_cast<size_t>(ply) * area);
+        toMove[ply] = static_cast<uint8_t>(b.toMove());
+        hashes[ply] = b.hash();
+        uint8_t* lg = legal + static_cast<size_t>(ply) * (area + 1);
+        for (int a = 0; a < area; ++a) lg[a] = b.isLegal(a) && !game.seen(b.hashAfter(a));
+        lg[area] = 1;
+        if (ply == moves || game.isTerminal()) return ply;
+        const std::vector<int> acts = game.legalActions();
+        const int points = static_cast<int>(acts.size()) - 1;
+        game.play(points > 0 ? acts[rng.below(points)] : acts.back());
+    }
+}
+
+// Board::isLegal, hashAfter and play on a position given as stones.
+static Board boardOf(const uint8_t* stones, int n, int toMove) {
+    Board b(n);
+    for (int p = 0; p < n * n; ++p) b.setStone(p, static_cast<Color>(stones[p]));
+    b.setToMove(toMove == 1 ? Color::Black : Color::White);
+    return b;
+}
+void ref_board_legal(const uint8_t* stones, int n, int toMove, uint8_t* legal) {
+    const Board b = boardOf(stones, n, toMove);
+    for (int a = 0; a <= n * n; ++a) legal[a] = b.isLegal(a);
+}
+void ref_hash_after(const uint8_t* stones, int n, int toMove, uint64_t* out) {
+    const Board b = boardOf(stones, n, toMove);
+    for (int a = 0; a <= n * n; ++a) out[a] = b.isLegal(a) ? b.hashAfter(a) : 0;
+}
+uint64_t ref_board_hash(const uint8_t* stones, int n) { return boardOf(stones, n, 1).hash(); }
 
 } // extern "C"

@@ -26,6 +26,11 @@ Vectors (data only, no reference source):
                   head (version 2)
   gen0_infer.npz  Network::infer of those two checkpoints as loadNetwork
                   reads them, on the 5x5 workload's batch of 8 positions
+  games.npz       random games played by the reference's Game with
+                  bnCalibrationPositions' move choice (src/bn_calibration.cpp:19-28):
+                  every position's stones, side to move, Board::hash and the
+                  legal set Mcts::expand builds at a root (src/mcts.cpp:152-169),
+                  on 5x5, 9x9, 13x13 and 19x19 boards
 """
 import hashlib
 import json
@@ -105,7 +110,24 @@ def main():
     np.savez_compressed(os.path.join(HERE, "infer_9x9_random.npz"), input=inp, logits=logits, values=values,
                         **tensors)
     calibrated()
+    games()
     print("golden vectors written to", HERE)
+
+
+# (board size, seeds, moves): lengths reach captures, ko fights (superko
+# exclusions) and, on 19x19, superko lists longer than 512 positions.
+GAMES = ((5, range(1, 11), 80), (9, range(1, 4), 200), (13, range(1, 2), 300), (19, range(1, 2), 600))
+
+
+def games():
+    out = {}
+    for n, seeds, moves in GAMES:
+        for seed in seeds:
+            stones, to_move, hashes, legal = O.random_game(n, seed, moves, ref=True)
+            key = f"{n}_{seed}"
+            out[key + "/stones"], out[key + "/to_move"] = stones, to_move
+            out[key + "/hashes"], out[key + "/legal"] = hashes, legal
+    np.savez_compressed(os.path.join(HERE, "games.npz"), **out)
 
 
 # Calibrated shapes: the workloads' networks (workload 4 is workload 3's)
@@ -145,5 +167,7 @@ def calibrated():
 if __name__ == "__main__":
     if sys.argv[1:] == ["calibrated"]:
         calibrated()
+    elif sys.argv[1:] == ["games"]:
+        games()
     else:
         main()
