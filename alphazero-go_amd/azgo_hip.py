@@ -93,6 +93,7 @@ def load():
             "azh_encode_planes": ([u8, P(C.c_int32), u8, u8, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_legal_moves": ([u8, C.c_int, u8, P(C.c_uint64), P(C.c_int64), C.c_int, u8], C.c_int),
             "azh_evaluate_positions": ([vp, P(Positions), C.c_int, f32, f32, u8, f32], C.c_int),
+            "azh_time_positions": ([vp, P(Positions), C.c_int, C.c_int, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_enqueue": ([vp, C.c_int, C.c_int], C.c_int),
@@ -304,17 +305,30 @@ class Runner:
         _check(self.lib.azh_infer(self.h, _f(inp), B, _f(logits), _f(values), _f(own) if ownership else None))
         return (logits, values, own) if ownership else (logits, values)
 
+    def _positions(self, stones, to_move, plies, sym, seen):
+        stones = np.ascontiguousarray(stones, np.uint8)
+        B = stones.shape[0]
+        keep = [stones, np.ascontiguousarray(to_move, np.uint8),
+                None if plies is None else np.ascontiguousarray(plies, np.int32),
+                None if sym is None else np.ascontiguousarray(sym, np.uint8)]
+        flat, offs = _seen_lists(seen, B)
+        keep += [flat, offs]
+        pos = Positions(_u8(keep[0]), None if keep[2] is None else keep[2].ctypes.data_as(C.POINTER(C.c_int32)),
+                        _u8(keep[1]), _u8(keep[3]), flat.ctypes.data_as(C.POINTER(C.c_uint64)),
+                        offs.ctypes.data_as(C.POINTER(C.c_int64)))
+        return B, pos, keep
+
+    def time_positions(self, stones, to_move, plies=None, sym=None, seen=None, iters=10):
+        """Total ms of `iters` runs of each step: (encode, legal, priors, whole chain)."""
+        B, pos, keep = self._positions(stones, to_move, plies, sym, seen)
+        ms = (C.c_float * 4)()
+        _check(self.lib.azh_time_positions(self.h, C.byref(pos), B, iters, ms))
+        return tuple(ms)
+
     def evaluate_positions(self, stones, to_move, plies=None, sym=None, seen=None):
         """The leaf evaluation on the GPU (azh_evaluate_positions): stones
         [B][H][area] bytes -> (logits mapped back, priors, legal, values)."""
-        stones = np.ascontiguousarray(stones, np.uint8)
-        B = stones.shape[0]
-        to_move = np.ascontiguousarray(to_move, np.uint8)
-        pl = None if plies is None else np.ascontiguousarray(plies, np.int32)
-        sy = None if sym is None else np.ascontiguousarray(sym, np.uint8)
-        flat, offs = _seen_lists(seen, B)
-        pos = Positions(_u8(stones), None if pl is None else pl.ctypes.data_as(C.POINTER(C.c_int32)), _u8(to_move),
-                        _u8(sy), flat.ctypes.data_as(C.POINTER(C.c_uint64)), offs.ctypes.data_as(C.POINTER(C.c_int64)))
+        B, pos, keep = self._positions(stones, to_move, plies, sym, seen)
         A1 = self.cfg.actions
         logits = np.empty((B, A1), np.float32)
         priors = np.empty((B, A1), np.float32)

@@ -21,9 +21,9 @@ SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip"]
 # workgroup shape): azh_conv_inst.hip is compiled once per pair, so the
 # fully unrolled kernels build in parallel.
 CONV_INST = "azh_conv_inst.hip"
-CONV_HEADERS = ["azh_conv.hpp", "azh_kernels.hpp"]
+CONV_HEADERS = ["azh_conv.hpp", "azh_conv_iface.hpp"]
 BOARD_SIZES = (5, 9, 13, 19)   # conv3x3Supported
-HEADERS = CONV_HEADERS + [os.path.join("..", "..", "include", "azgo_hip.h")]
+HEADERS = CONV_HEADERS + ["azh_kernels.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -57,8 +57,8 @@ def conv_hash():
 
 
 def conv_tiling_count():
-    """Entries of kConvTilings (azh_kernels.hpp)."""
-    text = open(os.path.join(CSRC, "azh_kernels.hpp")).read()
+    """Entries of kConvTilings (azh_conv_iface.hpp)."""
+    text = open(os.path.join(CSRC, "azh_conv_iface.hpp")).read()
     body = text[text.index("kConvTilings[] = {") + len("kConvTilings[] = {"):]
     body = body[:body.index("};")]
     return body.count("{")

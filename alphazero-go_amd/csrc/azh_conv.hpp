@@ -20,7 +20,7 @@
 // i + 16k, B[k][j] from lane j + 16k, and lane j + 16g holds D[4g + r][j] in
 // accumulator element r.
 #pragma once
-#include "azh_kernels.hpp"
+#include "azh_conv_iface.hpp"
 
 #include <hip/hip_runtime.h>
 

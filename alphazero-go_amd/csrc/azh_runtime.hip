@@ -499,6 +499,19 @@ size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
     return (size_t)slots * slotFloats(Shape(c), maxBatch) * sizeof(float) + weightFloats(c) * sizeof(float);
 }
 
+// A batch of positions staged on the device (azh_evaluate_positions).
+struct PositionsOnDevice {
+    const uint8_t* stones = nullptr;   // [B][H][A]
+    const int* plies = nullptr;        // [B]
+    const uint8_t* turn = nullptr;     // [B]
+    const uint8_t* sym = nullptr;      // [B]
+    const long long* offsets = nullptr;   // [B+1]
+    const uint64_t* seen = nullptr;
+    uint8_t* legal = nullptr;          // [B][A+1]
+    float* mapped = nullptr;           // [B][A+1]
+    float* priors = nullptr;           // [B][A+1]
+};
+
 // A device allocation released on scope exit (the synchronous kernel entry points).
 struct DeviceBuffer {
     void* p = nullptr;
@@ -571,6 +584,8 @@ struct Slot {
     // offsets, legal [maxBatch][A+1], mapped logits and priors, and the
     // concatenated superko hashes (grown as needed).
     GrowingBuffer posBytes, posSeen;
+    std::vector<int> posPlies;       // host copies the staging reads from
+    std::vector<uint8_t> posSym;
 
     Slot(const Shape& s, int maxBatch) {
         const size_t B = maxBatch;
@@ -736,6 +751,70 @@ struct azh_runner {
             it = s.graphs.emplace(B, exec).first;
         }
         check(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
+    }
+
+    // The positions path's device arrays for B positions in slot s, staged
+    // from the caller's (checked) host arrays on the slot's stream: the
+    // batch-sized parts in one allocation at maxBatch, the superko hashes in
+    // a buffer grown as needed.
+    PositionsOnDevice stagePositions(Slot& s, const azh_positions& pos, int B) {
+        const Shape& sh = shape;
+        const size_t A = sh.A, A1 = sh.A1, H = sh.H, M = maxBatch;
+        checkPositions(pos.stones, (size_t)B * H * A, pos.plies, pos.to_move, pos.sym, pos.seen_offsets, pos.seen, B,
+                       sh.H);
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t o = off;
+            off += (bytes + 255) / 256 * 256;
+            return o;
+        };
+        const size_t oStones = take(M * H * A), oPlies = take(M * sizeof(int)), oTurn = take(M), oSym = take(M),
+                     oOff = take((M + 1) * sizeof(int64_t)), oLegal = take(M * A1),
+                     oMapped = take(M * A1 * sizeof(float)), oPriors = take(M * A1 * sizeof(float));
+        uint8_t* base = static_cast<uint8_t*>(s.posBytes.reserve(off));
+        const size_t nSeen = (size_t)pos.seen_offsets[B];
+        uint64_t* seen = static_cast<uint64_t*>(s.posSeen.reserve(std::max<size_t>(nSeen, 1) * sizeof(uint64_t)));
+        s.posPlies.assign(B, sh.H);
+        if (pos.plies) std::copy(pos.plies, pos.plies + B, s.posPlies.begin());
+        s.posSym.assign(B, 0);
+        if (pos.sym) std::copy(pos.sym, pos.sym + B, s.posSym.begin());
+        auto up = [&](size_t o, const void* src, size_t bytes) {
+            check(hipMemcpyAsync(base + o, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(positions)");
+        };
+        up(oStones, pos.stones, (size_t)B * H * A);
+        up(oPlies, s.posPlies.data(), (size_t)B * sizeof(int));
+        up(oTurn, pos.to_move, B);
+        up(oSym, s.posSym.data(), B);
+        up(oOff, pos.seen_offsets, (size_t)(B + 1) * sizeof(int64_t));
+        if (nSeen)
+            check(hipMemcpyAsync(seen, pos.seen, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice, s.stream),
+                  "hipMemcpyAsync(seen)");
+        PositionsOnDevice d;
+        d.stones = base + oStones;
+        d.plies = reinterpret_cast<const int*>(base + oPlies);
+        d.turn = base + oTurn;
+        d.sym = base + oSym;
+        d.offsets = reinterpret_cast<const long long*>(base + oOff);
+        d.seen = seen;
+        d.legal = base + oLegal;
+        d.mapped = reinterpret_cast<float*>(base + oMapped);
+        d.priors = reinterpret_cast<float*>(base + oPriors);
+        return d;
+    }
+    // encodePlanes into the pass's input.
+    void encodeStep(Slot& s, const PositionsOnDevice& d, int B) {
+        check(azh::launchEncodePlanes(d.stones, d.plies, d.turn, d.sym, s.dIn, B, shape.n, shape.H, s.stream), "encode");
+    }
+    // The legal moves of each position's current board (ply 0 of its stones).
+    void legalStep(Slot& s, const PositionsOnDevice& d, int B) {
+        check(azh::launchLegalMoves(d.stones, (size_t)shape.H * shape.A, d.turn, d.seen, d.offsets, d.legal, B,
+                                    shape.n, s.stream),
+              "legal moves");
+    }
+    // The pass's logits mapped back from the symmetry, and the priors.
+    void priorsStep(Slot& s, const PositionsOnDevice& d, int B) {
+        check(azh::launchPriors(s.dLogits, d.legal, d.sym, d.mapped, d.priors, B, shape.A1, shape.n, s.stream),
+              "priors");
     }
 
     void copyIn(Slot& s, int B) {
@@ -1112,61 +1191,57 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
         if (!r || !pos || !priors || !legal || !values)
             throw Error(AZH_ERR_ARGUMENT, "hip: evaluate_positions needs its arrays");
         r->checkBatch(B);
-        const Shape& sh = r->shape;
-        const size_t A = sh.A, A1 = sh.A1, H = sh.H, M = r->maxBatch;
-        checkPositions(pos->stones, (size_t)B * H * A, pos->plies, pos->to_move, pos->sym, pos->seen_offsets,
-                       pos->seen, B, sh.H);
         Slot& s = r->idleSlot(0);
-        // One allocation for the batch-sized parts, at the runner's maxBatch.
-        size_t off = 0;
-        auto take = [&](size_t bytes) {
-            const size_t o = off;
-            off += (bytes + 255) / 256 * 256;
-            return o;
-        };
-        const size_t oStones = take(M * H * A), oPlies = take(M * sizeof(int)), oTurn = take(M), oSym = take(M),
-                     oOff = take((M + 1) * sizeof(int64_t)), oLegal = take(M * A1),
-                     oMapped = take(M * A1 * sizeof(float)), oPriors = take(M * A1 * sizeof(float));
-        uint8_t* base = static_cast<uint8_t*>(s.posBytes.reserve(off));
-        const size_t nSeen = (size_t)pos->seen_offsets[B];
-        uint64_t* dSeen = static_cast<uint64_t*>(s.posSeen.reserve(std::max<size_t>(nSeen, 1) * sizeof(uint64_t)));
-        std::vector<int> pl(B, sh.H);
-        if (pos->plies) std::copy(pos->plies, pos->plies + B, pl.begin());
-        std::vector<uint8_t> sy(B, 0);
-        if (pos->sym) std::copy(pos->sym, pos->sym + B, sy.begin());
-        auto up = [&](size_t o, const void* src, size_t bytes) {
-            check(hipMemcpyAsync(base + o, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(positions)");
-        };
-        up(oStones, pos->stones, (size_t)B * H * A);
-        up(oPlies, pl.data(), (size_t)B * sizeof(int));
-        up(oTurn, pos->to_move, B);
-        up(oSym, sy.data(), B);
-        up(oOff, pos->seen_offsets, (size_t)(B + 1) * sizeof(int64_t));
-        if (nSeen)
-            check(hipMemcpyAsync(dSeen, pos->seen, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice, s.stream),
-                  "hipMemcpyAsync(seen)");
-        const uint8_t* dStones = base + oStones;
-        const uint8_t* dTurn = base + oTurn;
-        const uint8_t* dSym = base + oSym;
-        uint8_t* dLegal = base + oLegal;
-        float* dMapped = reinterpret_cast<float*>(base + oMapped);
-        float* dPriors = reinterpret_cast<float*>(base + oPriors);
-        check(azh::launchEncodePlanes(dStones, reinterpret_cast<const int*>(base + oPlies), dTurn, dSym, s.dIn, B, sh.n,
-                                      sh.H, s.stream),
-              "encode");
+        const PositionsOnDevice d = r->stagePositions(s, *pos, B);
+        r->encodeStep(s, d, B);
         r->enqueuePass(s, B);
-        check(azh::launchLegalMoves(dStones, H * A, dTurn, dSeen, reinterpret_cast<const long long*>(base + oOff),
-                                    dLegal, B, sh.n, s.stream),
-              "legal moves");
-        check(azh::launchPriors(s.dLogits, dLegal, dSym, dMapped, dPriors, B, (int)A1, sh.n, s.stream), "priors");
+        r->legalStep(s, d, B);
+        r->priorsStep(s, d, B);
+        const size_t A1 = r->shape.A1;
         auto down = [&](void* dst, const void* src, size_t bytes) {
             check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(outputs)");
         };
-        down(priors, dPriors, (size_t)B * A1 * sizeof(float));
-        down(legal, dLegal, (size_t)B * A1);
+        down(priors, d.priors, (size_t)B * A1 * sizeof(float));
+        down(legal, d.legal, (size_t)B * A1);
         down(values, s.dValues, (size_t)B * sizeof(float));
-        if (logits) down(logits, dMapped, (size_t)B * A1 * sizeof(float));
+        if (logits) down(logits, d.mapped, (size_t)B * A1 * sizeof(float));
         check(hipStreamSynchronize(s.stream), "GPU inference failed");
+    });
+}
+
+int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters, float* ms) {
+    return guarded([&] {
+        if (!r || !pos || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(0);
+        const PositionsOnDevice d = r->stagePositions(s, *pos, B);
+        // One untimed run of everything (the pass's graph for B is captured here).
+        r->encodeStep(s, d, B);
+        r->enqueuePass(s, B);
+        r->legalStep(s, d, B);
+        r->priorsStep(s, d, B);
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        check(hipEventCreate(&e0), "hipEventCreate");
+        check(hipEventCreate(&e1), "hipEventCreate");
+        struct Events {
+            hipEvent_t a, b;
+            ~Events() {
+                (void)hipEventDestroy(a);
+                (void)hipEventDestroy(b);
+            }
+        } guard{e0, e1};
+        for (int step = 0; step < 4; ++step) {
+            check(hipEventRecord(e0, s.stream), "hipEventRecord");
+            for (int i = 0; i < iters; ++i) {
+                if (step == 0 || step == 3) r->encodeStep(s, d, B);
+                if (step == 3) r->enqueuePass(s, B);
+                if (step == 1 || step == 3) r->legalStep(s, d, B);
+                if (step == 2 || step == 3) r->priorsStep(s, d, B);
+            }
+            check(hipEventRecord(e1, s.stream), "hipEventRecord");
+            check(hipEventSynchronize(e1), "hipEventSynchronize");
+            check(hipEventElapsedTime(&ms[step], e0, e1), "hipEventElapsedTime");
+        }
     });
 }
 

@@ -65,6 +65,8 @@ def _lib():
         h.azw_network.argtypes = [i] * 5 + [C.c_uint64, C.POINTER(C.c_float)]
         h.azw_positions.argtypes = [i, i, i, C.c_uint64, C.c_uint64, C.c_double, C.c_double,
                                     C.POINTER(C.c_float), C.POINTER(C.c_uint8)]
+        h.azw_stones.argtypes = [i, i, C.c_uint64, C.c_uint64, C.c_double, C.c_double, C.POINTER(C.c_uint8),
+                                 C.POINTER(C.c_uint8)]
         _lib.h = h
     return _lib.h
 
@@ -102,3 +104,14 @@ def positions(w: Workload, B=None, seed=SEED):
     _lib().azw_positions(n, H, B, seed, w.tag, w.p_black, w.p_white,
                          inp.ctypes.data_as(C.POINTER(C.c_float)), legal.ctypes.data_as(C.POINTER(C.c_uint8)))
     return inp, legal
+
+
+def stones(w: Workload, B=None, seed=SEED):
+    """The same boards as positions(), as bytes: (stones [B][n*n], to_move [B])."""
+    B = w.batch if B is None else B
+    n = w.cfg[0]
+    st = np.empty((B, n * n), np.uint8)
+    tm = np.empty(B, np.uint8)
+    _lib().azw_stones(n, B, seed, w.tag, w.p_black, w.p_white, st.ctypes.data_as(C.POINTER(C.c_uint8)),
+                      tm.ctypes.data_as(C.POINTER(C.c_uint8)))
+    return st, tm

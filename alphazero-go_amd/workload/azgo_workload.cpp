@@ -213,4 +213,20 @@ void azw_positions(int n, int history, int B, uint64_t seed, uint64_t tag, doubl
     }
 }
 
+// The same boards as azw_positions, as bytes: stones [B][n*n] (0 empty,
+// 1 black, 2 white) and the side to move [B] (1 or 2).
+void azw_stones(int n, int B, uint64_t seed, uint64_t tag, double pBlack, double pWhite, uint8_t* stones,
+                uint8_t* toMove) {
+    const int A = n * n;
+    for (int i = 0; i < B; ++i) {
+        Xoshiro rng(Xoshiro::derive(seed, tag, static_cast<uint64_t>(i), 0));
+        uint8_t* s = stones + static_cast<size_t>(i) * A;
+        for (int p = 0; p < A; ++p) {
+            const double u = rng.uniform();
+            s[p] = u < pBlack ? 1 : (u < pBlack + pWhite ? 2 : 0);
+        }
+        toMove[i] = rng.below(2) == 0 ? 1 : 2;
+    }
+}
+
 } // extern "C"

@@ -9,7 +9,13 @@ convolution, timed live with HIP events on its stream), and the CPU
 baseline (the oracle's single-threaded blas pass, one worker per host core
 at batch 8, as the reference bench's "cpu (blas)" row).
 
-  python bench.py [--steps K] [--warmup W] [--workload 3] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload 3] [--no-cpu] [--no-positions]
+
+Beside the headline, "positions" times the steps either side of the pass
+(azh_evaluate_positions: encoding from stone bytes, the legal moves with
+superko, the priors) on the same boards, each position carrying 200
+superko hashes, with the oracle's CPU restatement of the same two steps
+timed on one host core.
 
 Runs on one GPU only: --gpus above 1 exits with a message.
 """
@@ -43,6 +49,8 @@ def parse():
     ap.add_argument("--conv-iters", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-calls", type=int, default=96, help="batch-8 passes per CPU worker")
+    ap.add_argument("--no-positions", action="store_true", help="skip the positions path")
+    ap.add_argument("--seen", type=int, default=200, help="superko hashes per position")
     return ap.parse_args()
 
 
@@ -95,6 +103,61 @@ def cpu_baseline(workload, calls):
     }
 
 
+def positions_leg(r, w, B, seen_per_position, iters=20):
+    """The positions path on the benchmark's boards (no history: ply 0 only),
+    device-resident: HIP events around each step (encode, legal moves,
+    priors) and the whole chain (encode, pass, legal moves, priors)."""
+    import numpy as np
+    import workload as W
+    n, H = w.cfg[0], w.cfg[1]
+    st, tm = W.stones(w, B)
+    hist = np.zeros((B, H, n * n), np.uint8)
+    hist[:, 0] = st
+    plies = np.ones(B, np.int32)
+    sym = (np.arange(B) % 8).astype(np.uint8)
+    g = np.random.default_rng(1)
+    seen = [g.integers(0, 2 ** 63, seen_per_position, dtype=np.int64).astype(np.uint64) for _ in range(B)]
+    enc, leg, pri, chain = (x / iters for x in r.time_positions(hist, tm, plies, sym, seen, iters))
+    A, P = n * n, 2 * H + 2
+    enc_bytes = B * (H * A + P * A * 4)                      # stone bytes in, planes out
+    leg_bytes = B * (A + (A + 1) + 8 * seen_per_position)    # boards and superko hashes in, masks out
+    return {
+        "workload": f"{n}x{n} batch {B}, the benchmark's boards, {seen_per_position} superko hashes each",
+        "encode_us": round(enc * 1e3, 2),
+        "legal_us": round(leg * 1e3, 2),
+        "priors_us": round(pri * 1e3, 2),
+        "chain_ms": round(chain, 4),
+        "chain_positions_per_s": round(B / (chain * 1e-3), 1),
+        "encode_gbs": round(enc_bytes / (enc * 1e-3) / 1e9, 1),
+        "legal_positions_per_s": round(B / (leg * 1e-3), 1),
+        "legal_gbs": round(leg_bytes / (leg * 1e-3) / 1e9, 2),
+        "_inputs": (st, tm, seen),
+    }
+
+
+def positions_cpu_baseline(w, st, tm, seen, H, budget_s=3.0):
+    """The oracle's encodePlanes + legal moves (Board::isLegal, hashAfter,
+    the superko scan) for the same positions on one host core."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    n = w.cfg[0]
+    t0 = time.perf_counter()
+    done = 0
+    while True:
+        for b in range(len(st)):
+            O.encode_planes(st[b:b + 1], n, int(tm[b]), H, b % 8)
+            O.legal_moves(st[b], n, int(tm[b]), seen[b])
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(done / el, 1), "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{done} positions in {el:.1f} s (oracle encodePlanes + legal moves with superko)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -142,6 +205,7 @@ def main():
         rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
         logits, values = r.fetch(0, B)
         assert (logits == logits).all() and (values == values).all(), "NaN in outputs"
+        pos = None if args.no_positions else positions_leg(r, w, B, args.seen)
 
     conv_flops = w.trunk_conv_flops(B)
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
@@ -189,6 +253,11 @@ def main():
         line["gpu_over_cpu"] = round(value / cb["value"], 1) if cb["value"] > 0 else None
     else:
         line["cpu_baseline"] = None
+    if pos is not None:
+        st, tm, seen = pos.pop("_inputs")
+        if not args.no_cpu:
+            pos["cpu_baseline"] = positions_cpu_baseline(w, st, tm, seen, H)
+        line["positions"] = pos
     print(json.dumps(line), flush=True)
 
 

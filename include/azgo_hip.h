@@ -224,6 +224,12 @@ typedef struct azh_positions {
 int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float* logits, float* priors,
                            uint8_t* legal, float* values);
 
+/* HIP events on slot 0's stream around `iters` device-resident runs of each
+ * step of azh_evaluate_positions, on positions staged once: ms[0] the
+ * encoding, ms[1] the legal moves, ms[2] the priors, ms[3] the whole chain
+ * (encoding, pass, legal moves, priors). Totals in milliseconds. */
+int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters, float* ms);
+
 /* Whether passes replay a captured hipGraph per batch size (default 1), or
  * launch their kernels one by one. */
 int azh_set_graphs(azh_runner* r, int enabled);

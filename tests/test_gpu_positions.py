@@ -186,3 +186,18 @@ def test_evaluate_positions_end_to_end(hip, n, tag):
     assert dp <= 1e-5
     assert np.all(priors[legal == 0] == 0)
     assert np.allclose(priors.sum(axis=1), 1.0, atol=1e-5)
+
+
+def test_time_positions_runs_each_step(hip):
+    net = calibrated_network("1")
+    n, H = 5, net.cfg.history
+    g = np.random.default_rng(3)
+    B = 8
+    stones = g.integers(0, 3, (B, H, n * n)).astype(np.uint8)
+    to_move = g.integers(1, 3, B).astype(np.uint8)
+    with hip.Runner(to_hip_cfg(hip, net.cfg), net.tensors(), B, 1) as r:
+        ms = r.time_positions(stones, to_move, iters=3)
+        assert all(x > 0 for x in ms) and ms[3] >= max(ms[:3])
+        # the slot is idle again: an evaluation after the timing works
+        logits, priors, legal, values = r.evaluate_positions(stones, to_move)
+    assert np.isfinite(logits).all() and np.isfinite(values).all()
