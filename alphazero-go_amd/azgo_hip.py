@@ -100,7 +100,7 @@ def load():
             "azh_synchronize": ([vp, C.c_int], C.c_int),
             "azh_fetch": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_time_passes": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
-            "azh_time_tower_convs": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int)], C.c_int),
+            "azh_time_tower_convs": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int), P(C.c_int)], C.c_int),
             "azh_time_round_trips": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    f32], C.c_int),
@@ -390,11 +390,11 @@ class Runner:
         return ms.value
 
     def time_tower_convs(self, slot, B, iters):
-        """(total ms, launches) of `iters` runs of the tower's convolutions."""
+        """(total ms, launches, layers) of `iters` runs of the tower."""
         ms = C.c_float()
-        n = C.c_int()
-        _check(self.lib.azh_time_tower_convs(self.h, slot, B, iters, C.byref(ms), C.byref(n)))
-        return ms.value, n.value
+        n, layers = C.c_int(), C.c_int()
+        _check(self.lib.azh_time_tower_convs(self.h, slot, B, iters, C.byref(ms), C.byref(n), C.byref(layers)))
+        return ms.value, n.value, layers.value
 
     def time_round_trips(self, slot, B, iters):
         ms = C.c_float()

@@ -704,12 +704,12 @@ struct azh_runner {
     // The pass's kernels on `stream`: stem, `blocksToRun` residual blocks
     // (the trunk updated in place: the second conv's epilogue reads the skip
     // at exactly the element it writes), then the heads when asked.
-    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+    // The residual tower's first `blocksToRun` blocks on slot s's trunk.
+    // Returns the number of launches.
+    int launchTower(Slot& s, int B, hipStream_t stream, int blocksToRun) {
         const Shape& sh = shape;
+        if (blocksToRun < 1) return 0;
         const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
-        check(azh::launchConv3x3(s.dIn, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, s.dX, B,
-                                 sh.n, sh.P, sh.F, true, t, stream),
-              "conv3x3 (stem)");
         for (int i = 0; i < blocksToRun; ++i) {
             const ConvW& a = weights.conv1[i];
             const ConvW& b = weights.conv2[i];
@@ -720,6 +720,16 @@ struct azh_runner {
                                      stream),
                   "conv3x3 (conv2)");
         }
+        return 2 * blocksToRun;
+    }
+
+    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+        const Shape& sh = shape;
+        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
+        check(azh::launchConv3x3(s.dIn, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, s.dX, B,
+                                 sh.n, sh.P, sh.F, true, t, stream),
+              "conv3x3 (stem)");
+        launchTower(s, B, stream, blocksToRun);
         if (heads)
             check(azh::launchHeads(s.dX, weights.heads, s.dAct, s.dLogits, s.dValues, s.dOwn, B, sh.n, sh.F, sh.V,
                                    stream),
@@ -1301,29 +1311,18 @@ int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms) {
     });
 }
 
-int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches) {
+int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches, int* layers) {
     return guarded([&] {
-        if (!r || !ms || !launches || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        if (!r || !ms || !launches || !layers || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
         r->checkBatch(B);
         Slot& s = r->idleSlot(slot);
-        const Shape& sh = r->shape;
-        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
         // The tower as the pass runs it: every block's two convolutions in
         // order, each reading the previous one's output.
-        *ms = timeOnStream(s.stream, iters, [&] {
-            for (int i = 0; i < sh.blocks; ++i) {
-                const ConvW& a = r->weights.conv1[i];
-                const ConvW& b = r->weights.conv2[i];
-                check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
-                                         s.stream),
-                      "conv3x3");
-                check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, t,
-                                         s.stream),
-                      "conv3x3");
-            }
-        });
-        *launches = iters * 2 * sh.blocks;
+        int per = 0;
+        *ms = timeOnStream(s.stream, iters, [&] { per = r->launchTower(s, B, s.stream, r->shape.blocks); });
+        *launches = iters * per;
+        *layers = iters * 2 * r->shape.blocks;
     });
 }
 

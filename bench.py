@@ -54,9 +54,9 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profile(workload_name, kernel_hash):
+def traffic_from_profile(workload_name, kernel_hash, kernel):
     """HBM bytes per launch of the tower convolution, from the committed
-    rocprofv3 counter summary of the same kernels, or None."""
+    rocprofv3 counter summary of the same kernel and sources, or None."""
     path = os.path.join(ROOT, "profiles", "conv3x3_tower_hbm_traffic.txt")
     if not os.path.exists(path):
         return None
@@ -66,7 +66,7 @@ def traffic_from_profile(workload_name, kernel_hash):
             if ":" in line and not line.startswith("#"):
                 k, v = line.split(":", 1)
                 vals[k.strip()] = v.strip()
-    if vals.get("kernels") != kernel_hash or vals.get("workload") != workload_name:
+    if vals.get("kernels") != kernel_hash or vals.get("workload") != workload_name or vals.get("kernel") != kernel:
         return None
     try:
         return float(vals["hbm_bytes_per_launch"])
@@ -199,21 +199,24 @@ def main():
         ev_ms = r.time_passes(0, B, args.steps) / args.steps
         # The dominant kernel: the residual tower's 3x3 convolutions, timed as
         # the pass runs them (every block's two launches in order).
-        tower_ms, launches = r.time_tower_convs(0, B, args.conv_iters)
+        tower_ms, launches, layers = r.time_tower_convs(0, B, args.conv_iters)
         conv_ms = tower_ms / launches
+        layers_per_launch = layers // launches
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
         rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
         logits, values = r.fetch(0, B)
         assert (logits == logits).all() and (values == values).all(), "NaN in outputs"
         pos = None if args.no_positions else positions_leg(r, w, B, args.seen)
 
-    conv_flops = w.trunk_conv_flops(B)
+    # One launch runs layers_per_launch layers of the tower (one).
+    conv_flops = w.trunk_conv_flops(B) * layers_per_launch
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
+    kernel_name = "conv3x3Tower (residual tower, one launch = one layer over the batch)"
     pass_tflops = w.flops_per_position() * B / (ms_per_step * 1e-3) / 1e12
     # "..., kernels <all> (conv <conv>)": the traffic profile is keyed by the convolution's own hash.
     kernel_hash = azgo_hip.describe().rsplit("(conv ", 1)[-1].rstrip(")")
     name = f"{n}x{n} {blocks}x{F} batch {B}"
-    traffic = traffic_from_profile(name, kernel_hash)
+    traffic = traffic_from_profile(name, kernel_hash, kernel_name.split(" ")[0])
 
     line = {
         "metric": "net evals (positions)/sec at 19x19 batch 256; % fp32-MFMA peak",
@@ -235,7 +238,7 @@ def main():
         "event_ms_per_step": round(ev_ms, 4),
         "round_trip_ms": round(rt_ms, 4),
         "roofline": {
-            "kernel": "conv3x3Tower (residual tower, one launch = one layer over the batch)",
+            "kernel": kernel_name,
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP32_MFMA_TFLOPS,
@@ -243,6 +246,7 @@ def main():
             "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": traffic,
             "avg_launch_ms": round(conv_ms, 4),
+            "per_layer_ms": round(tower_ms / layers, 4),
             "flops_per_launch": conv_flops,
         },
         "device": azgo_hip.describe(),

@@ -250,10 +250,11 @@ int azh_fetch(azh_runner* r, int slot, int B);
  * total milliseconds. */
 int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms);
 /* HIP events on the slot's stream around `iters` runs of the residual
- * tower's convolutions as the pass runs them (every block's two, in order,
- * on the slot's staged data): total ms and the number of launches timed,
- * for the dominant kernel's average launch time. */
-int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches);
+ * tower as the pass runs it (every block's two convolutions, in order, on
+ * the slot's staged data): total ms, the number of launches timed and the
+ * number of layers they ran, for the dominant kernel's average launch time. */
+int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches, int* layers);
+
 /* Events around `iters` synchronous round trips: pinned H2D, pass, D2H. */
 int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
 
