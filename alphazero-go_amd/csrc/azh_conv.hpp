@@ -39,151 +39,17 @@ struct Geo {
     static constexpr int BUF = 4 * HA;         // float4 units of one LDS buffer (4 groups)
 };
 
-// A workgroup computes one board's output channels [co tile] at column
-// groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
-// channels and PPW column groups (PPW = 0: all of them). MASKED: input
-// channels past cin are read as zeros (the stem's 2H+2 planes); without it
-// every chunk is whole (cin a multiple of 16).
-template <int N, int COW, int WCO, int WPG, int PPW0, bool MASKED>
-__device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
-                                            const float* __restrict__ scale, const float* __restrict__ shift,
-                                            const float* skip, float* y, int cin, int cout, int nq, int coTiles,
-                                            int pixTiles, int relu) {
+// The epilogue: y = relu?(scale * acc + shift (+ skip)), each operation
+// rounded on its own, for a lane's COW x PPW accumulators (channels cb0..,
+// column groups pg0..). The residual input may be the output buffer itself
+// (the block's second convolution writes over its input), so the compiler
+// cannot move a residual read above an earlier store: all of a lane's
+// residual values are read first, in one batch, then combined and stored.
+template <int N, int COW, int PPW>
+__device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const float* __restrict__ scale,
+                                             const float* __restrict__ shift, const float* skip, float* y, int b,
+                                             int cout, int cb0, int pg0, int k, int n16, int relu) {
     using G = Geo<N>;
-    constexpr int PPW = PPW0 == 0 ? G::NPG : PPW0;
-    constexpr int WAVES = WCO * WPG;
-    constexpr int THREADS = WAVES * 64;
-    constexpr int ITEMS = 4 * G::A;   // (channel group, point) pairs per chunk
-    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
-    __shared__ f4 lds[2 * G::BUF];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
-    // co tiles of one board run on the same XCD and share its L2.
-    const int total = gridDim.x;
-    const int wg = blockIdx.x;
-    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
-    const int tilesPerBoard = coTiles * pixTiles;
-    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
-    const int ct = tile / pixTiles, pt = tile % pixTiles;
-    const int cb0 = (ct * WCO + wave / WPG) * COW;
-    // This wave's first column group (a constant 0 when every wave covers the board).
-    const int pg0 = PPW0 == 0 ? 0 : (pt * WPG + wave % WPG) * PPW;
-    const int k = lane >> 4, n16 = lane & 15;
-
-    for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // Each lane's LDS read position per column group (float4 units), taps
-    // and buffers added as constants. Points past the board read a valid
-    // cell; their outputs are never stored.
-    int rofs[PPW];
-#pragma unroll
-    for (int j = 0; j < PPW; ++j) {
-        int p = (pg0 + j) * 16 + n16;
-        p = p < G::A ? p : G::A - 1;
-        rofs[j] = k * G::HA + (p / N) * G::H + (p % N);
-    }
-
-    const float* xb = x + (size_t)b * cin * G::A;
-    f4 stage[PER];
-    auto load = [&](int q) {
-#pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int it = tid + r * THREADS;
-            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (it < ITEMS) {
-                const int g = it / G::A, p = it - g * G::A;
-                const int c0 = q * 16 + 4 * g;
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (!MASKED || c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
-            }
-            stage[r] = v;
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int it = tid + r * THREADS;
-            if (it < ITEMS) {
-                const int g = it / G::A, p = it - g * G::A;
-                lds[buf * G::BUF + g * G::HA + (p / N + 1) * G::H + (p % N + 1)] = stage[r];
-            }
-        }
-    };
-
-    f4 acc[COW][PPW];
-#pragma unroll
-    for (int c = 0; c < COW; ++c)
-#pragma unroll
-        for (int j = 0; j < PPW; ++j) acc[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    load(0);
-    __syncthreads();   // the zero fill is complete before any interior store
-    store(0);
-    __syncthreads();
-
-    // The (tap, column group) steps of a chunk run as one unrolled stream:
-    // the B operand of step i + kRing is read from LDS while step i's MFMAs
-    // run, and each tap's A fragments are fetched from global memory one tap
-    // ahead, so neither read's latency stalls the matrix pipe. The sched
-    // group hints keep that interleave (a step's MFMAs, then the read kRing
-    // steps ahead) and pin each A fetch to the start of the tap before the
-    // one that uses it (left free, the scheduler sinks it next to its use
-    // to save four registers, and every tap then waits a full round trip).
-    constexpr int kRing = 4;
-    constexpr int STEPS = 9 * PPW;
-    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
-    auto loadA = [&](int q, int t, f4 (&a)[COW]) {
-#pragma unroll
-        for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
-    };
-    f4 aCur[COW], aNext[COW];
-    loadA(0, 0, aCur);
-    for (int q = 0; q < nq; ++q) {
-        // The last chunk fetches itself again in place of a next one (never
-        // stored), which keeps the step stream free of branches.
-        const int qn = q + 1 < nq ? q + 1 : q;
-        const f4* buf = lds + (q & 1) * G::BUF;
-        f4 ring[kRing];
-#pragma unroll
-        for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = buf[rofs[i % PPW] + tapOffset(i / PPW)];
-        __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);   // the ring's first reads
-#pragma unroll
-        for (int i = 0; i < STEPS; ++i) {
-            const int t = i / PPW, pg = i % PPW;
-            if (pg == 0) {
-                // The next tap's A fragments (tap 8: the next chunk's first),
-                // and at tap 0 after them the next chunk's board planes: the
-                // count of outstanding loads drains in issue order, so tap
-                // 1's wait for its fragments does not wait for the planes.
-                loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
-                __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);   // issued here, a tap ahead
-                if (t == 0) load(qn);
-            }
-            const f4 bv = ring[i % kRing];
-            if (i + kRing < STEPS)
-                ring[i % kRing] = buf[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int c = 0; c < COW; ++c)
-                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
-            if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
-            if (pg == PPW - 1) {
-#pragma unroll
-                for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
-            }
-        }
-        if (q + 1 < nq) store((q + 1) & 1);
-        __syncthreads();
-    }
-
-    // The residual input may be the output buffer itself (the block's
-    // second convolution writes over its input), so the compiler cannot
-    // move a residual read above an earlier store. All of a lane's residual
-    // values are read first, in one batch, then combined and stored.
     const float* skipb = skip ? skip + (size_t)b * cout * G::A : nullptr;
     float* yb = y + (size_t)b * cout * G::A;
     float sc[COW][4], sh[COW][4];
@@ -226,6 +92,206 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
             }
         }
     }
+}
+
+// A workgroup computes one board's output channels [co tile] at column
+// groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
+// channels and PPW column groups (PPW = 0: all of them). MASKED: input
+// channels past cin are read as zeros (the stem's 2H+2 planes); without it
+// every chunk is whole (cin a multiple of 16).
+template <int N, int COW, int WCO, int WPG, int PPW0, bool MASKED>
+__device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
+                                            const float* __restrict__ scale, const float* __restrict__ shift,
+                                            const float* skip, float* y, int cin, int cout, int nq, int coTiles,
+                                            int pixTiles, int relu) {
+    using G = Geo<N>;
+    constexpr int PPW = PPW0 == 0 ? G::NPG : PPW0;
+    constexpr int WAVES = WCO * WPG;
+    constexpr int THREADS = WAVES * 64;
+    // A workgroup that covers part of the board (a pixel tile of SPAN
+    // points) stages only the board rows its points and their 3x3
+    // neighbourhoods touch: at most (SPAN - 1) / N + 2 rows plus a halo row
+    // on each side.
+    constexpr int SPAN = WPG * PPW * 16;
+    constexpr int ROWS = PPW0 == 0 ? N : ((SPAN - 1) / N + 4 < N ? (SPAN - 1) / N + 4 : N);
+    constexpr int ITEMS = 4 * ROWS * N;   // (channel group, point) pairs per chunk, at most
+    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
+    // Small pixel tiles on the larger boards (the small batches' shapes at
+    // 13x13 and 19x19): a tap is only 4 x PPW MFMAs there, far shorter than
+    // a global load's round trip, so the A fragments are fetched a whole
+    // chunk ahead (the nine taps of chunk q+1 during chunk q) instead of one
+    // tap ahead, and the board planes two chunks ahead instead of one.
+    constexpr bool SMALL = PPW0 != 0 && PPW0 <= 2 && N >= 13;
+    __shared__ f4 lds[2 * G::BUF];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
+    // co tiles of one board run on the same XCD and share its L2.
+    const int total = gridDim.x;
+    const int wg = blockIdx.x;
+    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
+    const int tilesPerBoard = coTiles * pixTiles;
+    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
+    const int ct = tile / pixTiles, pt = tile % pixTiles;
+    const int cb0 = (ct * WCO + wave / WPG) * COW;
+    // This wave's first column group (a constant 0 when every wave covers the board).
+    const int pg0 = PPW0 == 0 ? 0 : (pt * WPG + wave % WPG) * PPW;
+    const int k = lane >> 4, n16 = lane & 15;
+
+    for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Each lane's LDS read position per column group (float4 units), taps
+    // and buffers added as constants. Points past the board read a valid
+    // cell; their outputs are never stored.
+    int rofs[PPW];
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) {
+        int p = (pg0 + j) * 16 + n16;
+        p = p < G::A ? p : G::A - 1;
+        rofs[j] = k * G::HA + (p / N) * G::H + (p % N);
+    }
+
+    // The staged rows: all of them for a whole-board workgroup; for a pixel
+    // tile, its points' rows and one more on each side (clamped to the
+    // board; the halo rows stay zero). Rows outside are never read.
+    int rowLo = 0, span = G::A;   // compile-time constants unless the tile is a part of the board
+    if (PPW0 != 0 && SPAN < G::A) {
+        const int p0 = pt * SPAN;
+        const int p1 = min(G::A, p0 + SPAN);
+        rowLo = max(0, p0 / N - 1);
+        span = (min(N - 1, (p1 - 1) / N + 1) - rowLo + 1) * N;
+    }
+    const int items = 4 * span, first = rowLo * N;
+
+    const float* xb = x + (size_t)b * cin * G::A;
+    f4 stage[PER], stage2[SMALL ? PER : 1];
+    auto load = [&](int q, f4* dst) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (it < items) {
+                const int g = it / span, p = first + it - g * span;
+                const int c0 = q * 16 + 4 * g;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (!MASKED || c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+            }
+            dst[r] = v;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            if (it < items) {
+                const int g = it / span, p = first + it - g * span;
+                lds[buf * G::BUF + g * G::HA + (p / N + 1) * G::H + (p % N + 1)] = stage[r];
+            }
+        }
+    };
+
+    f4 acc[COW][PPW];
+#pragma unroll
+    for (int c = 0; c < COW; ++c)
+#pragma unroll
+        for (int j = 0; j < PPW; ++j) acc[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    load(0, stage);
+    __syncthreads();   // the zero fill is complete before any interior store
+    store(0);
+    // Two chunks ahead: chunk 1 waits in `stage` while chunk 0 is multiplied
+    // (with one chunk, chunk 0 again, never stored).
+    if (SMALL) load(min(1, nq - 1), stage);
+    __syncthreads();
+
+    // The (tap, column group) steps of a chunk run as one unrolled stream:
+    // the B operand of step i + kRing is read from LDS while step i's MFMAs
+    // run, and each tap's A fragments are fetched from global memory one tap
+    // ahead, so neither read's latency stalls the matrix pipe. The sched
+    // group hints keep that interleave (a step's MFMAs, then the read kRing
+    // steps ahead) and pin each A fetch to the start of the tap before the
+    // one that uses it (left free, the scheduler sinks it next to its use
+    // to save four registers, and every tap then waits a full round trip).
+    constexpr int kRing = 4;
+    constexpr int STEPS = 9 * PPW;
+    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
+    auto loadA = [&](int q, int t, f4 (&a)[COW]) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
+    };
+    f4 aCur[COW], aNext[COW];
+    f4 aChunk[SMALL ? 9 : 1][COW], aChunkNext[SMALL ? 9 : 1][COW];
+    if (SMALL) {
+#pragma unroll
+        for (int t = 0; t < 9; ++t) loadA(0, t, aChunk[t]);
+    } else {
+        loadA(0, 0, aCur);
+    }
+    for (int q = 0; q < nq; ++q) {
+        // The last chunks fetch the last one again in place of chunks that
+        // do not exist (never stored), which keeps the step stream free of
+        // branches.
+        const int qn = q + 1 < nq ? q + 1 : q;
+        const int q2 = q + 2 < nq ? q + 2 : nq - 1;
+        const f4* buf = lds + (q & 1) * G::BUF;
+        f4 ring[kRing];
+#pragma unroll
+        for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = buf[rofs[i % PPW] + tapOffset(i / PPW)];
+        __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);   // the ring's first reads
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+            const int t = i / PPW, pg = i % PPW;
+            if (pg == 0) {
+                // The next tap's A fragments (tap 8: the next chunk's first;
+                // SMALL: this tap's of the next chunk), and at tap 0 after
+                // them the board planes of the next chunk (SMALL: the one
+                // after it; the next waits in `stage`): the count of
+                // outstanding loads drains in issue order, so a tap's wait
+                // for its fragments does not wait for the planes.
+                if (SMALL)
+                    loadA(qn, t, aChunkNext[t]);
+                else
+                    loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
+                __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);   // issued here, a tap ahead
+                if (t == 0) {
+                    if (SMALL)
+                        load(q2, stage2);
+                    else
+                        load(qn, stage);
+                }
+            }
+            const f4 bv = ring[i % kRing];
+            if (i + kRing < STEPS)
+                ring[i % kRing] = buf[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int c = 0; c < COW; ++c)
+                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(SMALL ? aChunk[t][c][j] : aCur[c][j], bv[j],
+                                                                      acc[c][pg], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
+            if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
+            if (!SMALL && pg == PPW - 1) {
+#pragma unroll
+                for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
+            }
+        }
+        if (SMALL) {
+#pragma unroll
+            for (int t = 0; t < 9; ++t)
+#pragma unroll
+                for (int c = 0; c < COW; ++c) aChunk[t][c] = aChunkNext[t][c];
+        }
+        if (q + 1 < nq) store((q + 1) & 1);
+        if (SMALL) {
+#pragma unroll
+            for (int r = 0; r < PER; ++r) stage[r] = stage2[r];
+        }
+        __syncthreads();
+    }
+
+    storeOutputs<N, COW, PPW>(acc, scale, shift, skip, y, b, cout, cb0, pg0, k, n16, relu);
 }
 
 // The residual tower's convolutions (cin = filters, a multiple of 16) and
