@@ -6,7 +6,8 @@
 // position (board) and a tile of output channels. For each chunk of 16
 // input channels it stages the board's planes in LDS with a one-point zero
 // halo ((n+2) x (n+2) per channel, four channels interleaved per point so a
-// lane fetches four K values with one ds_read_b128); the nine taps are then
+// lane fetches four K values with one ds_read_b128, as the trunk's channel
+// quads already hold them in global memory); the nine taps are then
 // constant offsets into that tile, so the inner loop is LDS reads with
 // immediate offsets and MFMAs, and the im2col matrix never exists. The
 // chunks are double-buffered: the next chunk's global loads are in flight
@@ -14,7 +15,7 @@
 // fragment order straight from global memory (one coalesced dwordx4 per lane
 // per fragment quad; every workgroup reads the same 0.6 MB per layer, which
 // stays in L2). BN (scale, shift), the residual add and ReLU are applied to
-// the accumulators before the single store.
+// the accumulators before the single store of each channel quad.
 //
 // MFMA operand layout (16x16x4 f32, wave64): A[i][k] comes from lane
 // i + 16k, B[k][j] from lane j + 16k, and lane j + 16g holds D[4g + r][j] in
@@ -41,17 +42,23 @@ struct Geo {
 
 // The epilogue: y = relu?(scale * acc + shift (+ skip)), each operation
 // rounded on its own, for a lane's COW x PPW accumulators (channels cb0..,
-// column groups pg0..). The residual input may be the output buffer itself
-// (the block's second convolution writes over its input), so the compiler
-// cannot move a residual read above an earlier store: all of a lane's
-// residual values are read first, in one batch, then combined and stored.
+// column groups pg0..). A lane's four accumulators of a block are the four
+// channels of one quad at one point, so each output (and each residual
+// value) moves as one 16-byte access in the channel-quad layout; channels
+// past cout in the last quad are written as zeros. The residual input may be
+// the output buffer itself (the block's second convolution writes over its
+// input), so the compiler cannot move a residual read above an earlier
+// store: all of a lane's residual quads are read first, in one batch, then
+// combined and stored.
 template <int N, int COW, int PPW>
 __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const float* __restrict__ scale,
                                              const float* __restrict__ shift, const float* skip, float* y, int b,
                                              int cout, int cb0, int pg0, int k, int n16, int relu) {
     using G = Geo<N>;
-    const float* skipb = skip ? skip + (size_t)b * cout * G::A : nullptr;
-    float* yb = y + (size_t)b * cout * G::A;
+    const int quads = (cout + 3) / 4;
+    const size_t board = (size_t)b * quads * G::A;   // in float4 units
+    const f4* skipq = skip ? reinterpret_cast<const f4*>(skip) + board : nullptr;
+    f4* yq = reinterpret_cast<f4*>(y) + board;
     float sc[COW][4], sh[COW][4];
 #pragma unroll
     for (int c = 0; c < COW; ++c)
@@ -62,44 +69,43 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
             sh[c][r] = shift[co];
         }
     f4 res[COW][PPW];
-    if (skipb) {
+    if (skipq) {
 #pragma unroll
         for (int c = 0; c < COW; ++c)
 #pragma unroll
-            for (int j = 0; j < PPW; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // Lanes past the board or past cout read a valid cell;
-                    // their values are never stored.
-                    const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
-                    const int p = min((pg0 + j) * 16 + n16, G::A - 1);
-                    res[c][j][r] = skipb[(size_t)co * G::A + p];
-                }
+            for (int j = 0; j < PPW; ++j) {
+                // Lanes past the board or past cout read a valid quad; their
+                // values are never stored.
+                const int g = min((cb0 + c) * 4 + k, quads - 1);
+                const int p = min((pg0 + j) * 16 + n16, G::A - 1);
+                res[c][j] = skipq[(size_t)g * G::A + p];
+            }
     }
 #pragma unroll
     for (int c = 0; c < COW; ++c) {
-        const int coBase = (cb0 + c) * 16 + 4 * k;
+        const int g = (cb0 + c) * 4 + k;
+        if (g >= quads) continue;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int co = coBase + r;
-            if (co >= cout) continue;
+        for (int j = 0; j < PPW; ++j) {
+            const int p = (pg0 + j) * 16 + n16;
+            f4 o;
 #pragma unroll
-            for (int j = 0; j < PPW; ++j) {
-                const int p = (pg0 + j) * 16 + n16;
-                if (p < G::A)
-                    yb[(size_t)co * G::A + p] =
-                        epilogue(acc[c][j][r], sc[c][r], sh[c][r], skipb != nullptr, res[c][j][r], relu != 0);
-            }
+            for (int r = 0; r < 4; ++r)
+                o[r] = 4 * g + r < cout ? epilogue(acc[c][j][r], sc[c][r], sh[c][r], skipq != nullptr, res[c][j][r],
+                                                   relu != 0)
+                                        : 0.0f;
+            if (p < G::A) yq[(size_t)g * G::A + p] = o;
         }
     }
 }
 
 // A workgroup computes one board's output channels [co tile] at column
 // groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
-// channels and PPW column groups (PPW = 0: all of them). MASKED: input
-// channels past cin are read as zeros (the stem's 2H+2 planes); without it
-// every chunk is whole (cin a multiple of 16).
-template <int N, int COW, int WCO, int WPG, int PPW0, bool MASKED>
+// channels and PPW column groups (PPW = 0: all of them). PLANAR: x is the
+// network's input planes [B][cin][A] (the stem), read a channel at a time;
+// otherwise x is a trunk activation in channel quads, read a quad at a time.
+// Either way input channels past cin are read as zeros.
+template <int N, int COW, int WCO, int WPG, int PPW0, bool PLANAR>
 __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
                                             const float* __restrict__ scale, const float* __restrict__ shift,
                                             const float* skip, float* y, int cin, int cout, int nq, int coTiles,
@@ -163,7 +169,8 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     }
     const int items = 4 * span, first = rowLo * N;
 
-    const float* xb = x + (size_t)b * cin * G::A;
+    const float* xb = x + (size_t)b * cin * G::A;                                  // PLANAR
+    const f4* xq = reinterpret_cast<const f4*>(x) + (size_t)b * ((cin + 3) / 4) * G::A;   // channel quads
     f4 stage[PER], stage2[SMALL ? PER : 1];
     auto load = [&](int q, f4* dst) {
 #pragma unroll
@@ -173,9 +180,14 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
             if (it < items) {
                 const int g = it / span, p = first + it - g * span;
                 const int c0 = q * 16 + 4 * g;
+                if (PLANAR) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (!MASKED || c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+                    for (int c = 0; c < 4; ++c)
+                        if (c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+                } else if (c0 < cin) {
+                    // A quad's channels past cin are stored zeros.
+                    v = xq[(size_t)(c0 / 4) * G::A + p];
+                }
             }
             dst[r] = v;
         }
@@ -294,11 +306,11 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     storeOutputs<N, COW, PPW>(acc, scale, shift, skip, y, b, cout, cb0, pg0, k, n16, relu);
 }
 
-// The residual tower's convolutions (cin = filters, a multiple of 16) and
-// the stem's (cin = 2H+2 input planes) are separate kernels, so profiles
-// tell them apart. Two waves per SIMD are asked for where the whole
+// The residual tower's convolutions (input in channel quads) and the
+// stem's (input: the network's 2H+2 planes) are separate kernels, so
+// profiles tell them apart. Two waves per SIMD are asked for where the whole
 // workgroup shape allows it (one 16-channel block per wave).
-#define AZH_CONV_KERNEL(NAME, MASKED)                                                                      \
+#define AZH_CONV_KERNEL(NAME, PLANAR)                                                                      \
     template <int N, int COW, int WCO, int WPG, int PPW>                                                  \
     __global__ __launch_bounds__(WCO* WPG * 64)                                                          \
         __attribute__((amdgpu_waves_per_eu(COW == 1 && WCO * WPG >= 4 ? 2 : 1,                           \
@@ -306,7 +318,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         NAME(const float* __restrict__ x, const f4* __restrict__ wp, const float* __restrict__ scale,      \
              const float* __restrict__ shift, const float* skip, float* y, int cin, int cout, int nq,      \
              int coTiles, int pixTiles, int relu) {                                                        \
-        conv3x3Body<N, COW, WCO, WPG, PPW, MASKED>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,   \
+        conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,   \
                                                    pixTiles, relu);                                        \
     }
 AZH_CONV_KERNEL(conv3x3Tower, false)
@@ -317,14 +329,14 @@ AZH_CONV_KERNEL(conv3x3Stem, true)
 
 template <int N, int COW, int WCO, int WPG, int PPW>
 hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
-                       float* y, int B, int cin, int cout, bool relu, hipStream_t stream) {
+                       float* y, int B, int cin, int cout, bool relu, bool planarInput, hipStream_t stream) {
     constexpr int NPG = Geo<N>::NPG;
     constexpr int pgPerWave = PPW == 0 ? NPG : PPW;
     const int coTiles = ceilDiv(cout, 16 * COW * WCO);
     const int pixTiles = ceilDiv(NPG, WPG * pgPerWave);
     const int nq = ceilDiv(cin, kChunk);
     const dim3 grid(B * coTiles * pixTiles), block(WCO * WPG * 64);
-    if (cin % kChunk == 0)
+    if (!planarInput)
         hipLaunchKernelGGL((conv3x3Tower<N, COW, WCO, WPG, PPW>), grid, block, 0, stream, x,
                            reinterpret_cast<const f4*>(wp), scale, shift, skip, y, cin, cout, nq, coTiles, pixTiles,
                            relu ? 1 : 0);

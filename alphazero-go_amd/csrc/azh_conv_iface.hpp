@@ -55,20 +55,36 @@ constexpr ConvTiling kConvTilings[] = {{2, 2, 2, 12}, {1, 4, 1, 0}, {1, 2, 1, 0}
                                        {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1}};
 constexpr int kConvTilingCount = sizeof kConvTilings / sizeof kConvTilings[0];
 
+// Trunk activations (every convolution's output, the residual input and the
+// tower's input) are stored in channel quads: [B][ceil(C/4)][n*n][4], the
+// four channels 4g..4g+3 of a point side by side. A lane then moves four
+// channels with one 16-byte access: the LDS staging wants exactly that
+// interleave, and an MFMA lane's accumulators are four consecutive channels
+// of one point. Channels past C in the last quad are stored as zeros. The
+// network's input planes stay [B][P][n*n], as the reference hands them over.
+inline int channelQuads(int channels) { return ceilDiv(channels, 4); }
+inline size_t quadFloats(int B, int channels, int points) { return (size_t)B * channelQuads(channels) * 4 * points; }
+
+// Reorders between the planar [B][C][A] layout and channel quads (zeros in
+// the padding), on the host: for test hooks that take or return planar data.
+std::vector<float> toChannelQuads(const float* planar, int B, int C, int A);
+void fromChannelQuads(const float* quads, int B, int C, int A, float* planar);
+
 // One (board size, workgroup shape) instance of the convolution; defined in
 // azh_conv.hpp and instantiated by azh_conv_inst.hip, one object per shape.
 template <int N, int COW, int WCO, int WPG, int PPW>
 hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
-                       float* y, int B, int cin, int cout, bool relu, hipStream_t stream);
+                       float* y, int B, int cin, int cout, bool relu, bool planarInput, hipStream_t stream);
 
 // y[b][co][p] = relu?( (scale[co] * conv(x)[b][co][p] + shift[co]) (+ skip[b][co][p]) )
 // with each multiply and add rounded separately (BatchNorm2d::forwardInfer,
 // src/layers.cpp:88-97, then the skip add and reluForward,
 // src/network.cpp:264-271). skip may alias y (in-place residual).
-// x [B][cin][n*n], y and skip [B][cout][n*n].
+// y and skip in channel quads. x: planarInput, the network's input planes
+// [B][cin][n*n] (the stem); otherwise a trunk activation in channel quads.
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
-                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, ConvTiling tiling,
-                         hipStream_t stream);
+                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, bool planarInput,
+                         ConvTiling tiling, hipStream_t stream);
 bool conv3x3Supported(int boardSize);
 
 // y = relu?(scale * acc + shift (+ skip)), each operation rounded on its own.

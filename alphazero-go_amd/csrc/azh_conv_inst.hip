@@ -13,6 +13,7 @@ namespace azh {
 constexpr ConvTiling kInstTiling = kConvTilings[AZH_CONV_TILING];
 template hipError_t launchConvT<AZH_CONV_N, kInstTiling.coPerWave, kInstTiling.wavesCo, kInstTiling.wavesPg,
                                 kInstTiling.pgPerWave>(const float*, const float*, const float*, const float*,
-                                                       const float*, float*, int, int, int, bool, hipStream_t);
+                                                       const float*, float*, int, int, int, bool, bool,
+                                                       hipStream_t);
 
 } // namespace azh

@@ -22,13 +22,15 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // Picks the compiled instance of tiling t for board size N.
 template <int N, int I = 0>
 hipError_t launchConvN(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,
-                       float* y, int B, int cin, int cout, bool relu, ConvTiling t, hipStream_t stream) {
+                       float* y, int B, int cin, int cout, bool relu, bool planarInput, ConvTiling t,
+                       hipStream_t stream) {
     if constexpr (I < kConvTilingCount) {
         constexpr ConvTiling c = kConvTilings[I];
         if (t == c)
             return launchConvT<N, c.coPerWave, c.wavesCo, c.wavesPg, c.pgPerWave>(x, wp, scale, shift, skip, y, B,
-                                                                                  cin, cout, relu, stream);
-        return launchConvN<N, I + 1>(x, wp, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+                                                                                  cin, cout, relu, planarInput,
+                                                                                  stream);
+        return launchConvN<N, I + 1>(x, wp, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
     } else {
         return hipErrorInvalidValue;
     }
@@ -38,7 +40,8 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
 // and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
-// one point per thread, loads hoisted 16 channels ahead of their FMAs:
+// one point per thread, the trunk read in channel quads (four 16-byte loads
+// per 16 channels) ahead of their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
 // src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
 // ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
@@ -51,12 +54,17 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
     const int b = blockIdx.x, p = threadIdx.x;
     if (p >= A) return;
     const bool withOwn = own != nullptr;
-    const float* tb = trunk + (size_t)b * F * A + p;
+    const int quads = (F + 3) / 4;
+    const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + p;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     for (int c0 = 0; c0 < F; c0 += 16) {
         float xv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) xv[u] = c0 + u < F ? tb[(size_t)(c0 + u) * A] : 0.0f;
+        for (int g = 0; g < 4; ++g) {
+            const f4 v = c0 / 4 + g < quads ? tq[(size_t)(c0 / 4 + g) * A] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xv[4 * g + r] = v[r];
+        }
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             if (c0 + u < F) {
@@ -227,16 +235,34 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
 }
 
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
-                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, ConvTiling t,
-                         hipStream_t stream) {
+                         const float* skip, float* y, int B, int n, int cin, int cout, bool relu, bool planarInput,
+                         ConvTiling t, hipStream_t stream) {
     if (B < 1) return hipSuccess;
     switch (n) {
-    case 5: return launchConvN<5>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
-    case 9: return launchConvN<9>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
-    case 13: return launchConvN<13>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
-    case 19: return launchConvN<19>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, t, stream);
+    case 5: return launchConvN<5>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
+    case 9: return launchConvN<9>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
+    case 13: return launchConvN<13>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
+    case 19: return launchConvN<19>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+std::vector<float> toChannelQuads(const float* planar, int B, int C, int A) {
+    const int Q = channelQuads(C);
+    std::vector<float> out(quadFloats(B, C, A), 0.0f);
+    for (int b = 0; b < B; ++b)
+        for (int c = 0; c < C; ++c)
+            for (int p = 0; p < A; ++p)
+                out[(((size_t)b * Q + c / 4) * A + p) * 4 + c % 4] = planar[((size_t)b * C + c) * A + p];
+    return out;
+}
+
+void fromChannelQuads(const float* quads, int B, int C, int A, float* planar) {
+    const int Q = channelQuads(C);
+    for (int b = 0; b < B; ++b)
+        for (int c = 0; c < C; ++c)
+            for (int p = 0; p < A; ++p)
+                planar[((size_t)b * C + c) * A + p] = quads[(((size_t)b * Q + c / 4) * A + p) * 4 + c % 4];
 }
 
 hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values,

@@ -491,7 +491,7 @@ void uploadWeights(const azh_netcfg& c, const std::map<std::string, const float*
 
 size_t slotFloats(const Shape& s, int maxBatch) {
     const size_t B = maxBatch;
-    return alignFloats(B * s.P * s.A) + 2 * alignFloats(B * s.F * s.A) + alignFloats(B * 3 * s.A) +
+    return alignFloats(B * s.P * s.A) + 2 * alignFloats(azh::quadFloats(B, s.F, s.A)) + alignFloats(B * 3 * s.A) +
            alignFloats(B * s.A1) + alignFloats(B) + (s.ownership ? alignFloats(B * s.A) : 0);
 }
 
@@ -599,8 +599,8 @@ struct Slot {
             return p;
         };
         dIn = take(B * s.P * s.A);
-        dX = take(B * s.F * s.A);
-        dMid = take(B * s.F * s.A);
+        dX = take(azh::quadFloats(B, s.F, s.A));     // trunk activations in channel quads
+        dMid = take(azh::quadFloats(B, s.F, s.A));
         dAct = take(B * 3 * s.A);
         dLogits = take(B * s.A1);
         dValues = take(B);
@@ -713,11 +713,11 @@ struct azh_runner {
         for (int i = 0; i < blocksToRun; ++i) {
             const ConvW& a = weights.conv1[i];
             const ConvW& b = weights.conv2[i];
-            check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, t,
-                                     stream),
+            check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, false,
+                                     t, stream),
                   "conv3x3 (conv1)");
-            check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, t,
-                                     stream),
+            check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, false,
+                                     t, stream),
                   "conv3x3 (conv2)");
         }
         return 2 * blocksToRun;
@@ -727,7 +727,7 @@ struct azh_runner {
         const Shape& sh = shape;
         const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
         check(azh::launchConv3x3(s.dIn, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, s.dX, B,
-                                 sh.n, sh.P, sh.F, true, t, stream),
+                                 sh.n, sh.P, sh.F, true, true, t, stream),
               "conv3x3 (stem)");
         launchTower(s, B, stream, blocksToRun);
         if (heads)
@@ -1353,7 +1353,15 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
         requireContext();
         const size_t A = (size_t)n * n;
         const std::vector<float> packed = azh::packConv3x3(w, cin, cout);
-        const size_t fx = B * cin * A, fy = B * cout * A;
+        // The pass's two input layouts: a channel count that fills whole
+        // 16-channel chunks is tried as a trunk activation (channel quads,
+        // the tower kernel), any other as input planes (the stem kernel).
+        // Outputs and residuals are channel quads; the probe's own arrays
+        // are planar, converted here.
+        const bool planarIn = cin % azh::kChunk != 0;
+        const std::vector<float> xq = planarIn ? std::vector<float>() : azh::toChannelQuads(x, B, cin, (int)A);
+        const std::vector<float> kq = skip ? azh::toChannelQuads(skip, B, cout, (int)A) : std::vector<float>();
+        const size_t fx = planarIn ? B * cin * A : xq.size(), fy = azh::quadFloats(B, cout, (int)A);
         std::vector<float*> bufs;
         auto dev = [&](size_t floats) {
             float* p = nullptr;
@@ -1373,13 +1381,16 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
         float* dh = dev(cout);
         float* dy = dev(fy);
         float* dk = skip ? dev(fy) : nullptr;
-        check(hipMemcpy(dx, x, fx * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(hipMemcpy(dx, planarIn ? x : xq.data(), fx * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
         check(hipMemcpy(dw, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
         check(hipMemcpy(ds, scale, cout * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
         check(hipMemcpy(dh, shift, cout * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
-        if (dk) check(hipMemcpy(dk, skip, fy * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
-        check(azh::launchConv3x3(dx, dw, ds, dh, dk, dy, B, n, cin, cout, relu != 0, t, nullptr), "conv3x3");
-        check(hipMemcpy(y, dy, fy * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+        if (dk) check(hipMemcpy(dk, kq.data(), fy * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        check(azh::launchConv3x3(dx, dw, ds, dh, dk, dy, B, n, cin, cout, relu != 0, planarIn, t, nullptr),
+              "conv3x3");
+        std::vector<float> yq(fy);
+        check(hipMemcpy(yq.data(), dy, fy * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+        azh::fromChannelQuads(yq.data(), B, cout, (int)A, y);
     });
 }
 
@@ -1412,18 +1423,22 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
             bufs.push_back(p);
             return p;
         };
-        float* dx = dev(B * cin * A);
+        const bool planarIn = cin % azh::kChunk != 0;   // as azh_probe_conv3x3 chooses
+        const size_t fx = planarIn ? B * cin * A : azh::quadFloats(B, cin, (int)A);
+        float* dx = dev(fx);
         float* dw = dev(packed.size());
         float* ds = dev(cout);
         float* dh = dev(cout);
-        float* dy = dev(B * cout * A);
-        check(azh::launchFill(dx, B * cin * A, 0.5f, nullptr), "fill");
+        float* dy = dev(azh::quadFloats(B, cout, (int)A));
+        check(azh::launchFill(dx, fx, 0.5f, nullptr), "fill");
         check(azh::launchFill(ds, cout, 1.0f, nullptr), "fill");
         check(azh::launchFill(dh, cout, 0.0f, nullptr), "fill");
         check(hipMemcpy(dw, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
-        check(azh::launchConv3x3(dx, dw, ds, dh, nullptr, dy, B, n, cin, cout, true, t, nullptr), "conv3x3");
+        check(azh::launchConv3x3(dx, dw, ds, dh, nullptr, dy, B, n, cin, cout, true, planarIn, t, nullptr),
+              "conv3x3");
         *ms = timeOnStream(nullptr, iters, [&] {
-            check(azh::launchConv3x3(dx, dw, ds, dh, dy, dy, B, n, cin, cout, true, t, nullptr), "conv3x3");
+            check(azh::launchConv3x3(dx, dw, ds, dh, dy, dy, B, n, cin, cout, true, planarIn, t, nullptr),
+                  "conv3x3");
         });
     });
 }
@@ -1435,7 +1450,8 @@ int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, flo
         r->checkBatch(B);
         Slot& s = r->idleSlot(0);
         const Shape& sh = r->shape;
-        check(hipMemcpyAsync(s.dX, trunk, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
+        const std::vector<float> tq = azh::toChannelQuads(trunk, B, sh.F, sh.A);
+        check(hipMemcpyAsync(s.dX, tq.data(), tq.size() * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
         check(azh::launchHeads(s.dX, r->weights.heads, s.dAct, s.dLogits, s.dValues, s.dOwn, B, sh.n, sh.F, sh.V,
                                s.stream),
@@ -1461,9 +1477,11 @@ int azh_probe_trunk(azh_runner* r, const float* input, int B, int blocks, float*
         check(hipMemcpyAsync(s.dIn, input, (size_t)B * sh.P * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
         r->launchPass(s, B, s.stream, blocks, false);
-        check(hipMemcpyAsync(trunk, s.dX, (size_t)B * sh.F * sh.A * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+        std::vector<float> tq(azh::quadFloats(B, sh.F, sh.A));
+        check(hipMemcpyAsync(tq.data(), s.dX, tq.size() * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");
         check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+        azh::fromChannelQuads(tq.data(), B, sh.F, sh.A, trunk);
     });
 }
 

@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [  # (n, cin, cout, B): stem and tower shapes of the five workloads, plus ragged ones
     (5, 18, 32, 3), (5, 32, 32, 8), (9, 18, 64, 2), (9, 64, 64, 5), (19, 18, 128, 2), (19, 128, 128, 3),
-    (19, 256, 256, 1), (13, 40, 24, 2), (19, 7, 20, 2),
+    (19, 256, 256, 1), (13, 40, 24, 2), (19, 7, 20, 2), (9, 32, 30, 3), (5, 16, 18, 2),
 ]
 
 

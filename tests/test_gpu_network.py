@@ -89,6 +89,11 @@ def test_wide_net_vs_double(hip):
     (O.make_cfg(19, 10, 128, value_hidden=256), (1, 2)),
     (O.make_cfg(19, 2, 48), (3,)),
     (O.make_cfg(9, 0, 16), (5,)),
+    # filters that leave the last 16-channel chunk or the last channel quad
+    # part-filled, and input planes that fill whole chunks (history 7)
+    (O.make_cfg(9, 2, 20), (1, 5)),
+    (O.make_cfg(5, 2, 30, value_hidden=16), (3,)),
+    (O.make_cfg(5, 1, 32, history=7), (2,)),
 ])
 def test_random_networks_vs_double(hip, cfg, Bs):
     """tests/test_cuda.cpp:804-849 on random networks (random BN, biases):
