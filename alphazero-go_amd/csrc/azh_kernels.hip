@@ -40,8 +40,8 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
 // and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
-// one point per thread, the trunk read in channel quads (four 16-byte loads
-// per 16 channels) ahead of their FMAs:
+// one point per thread, the trunk read in channel quads (eight 16-byte loads
+// per 32 channels) ahead of their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
 // src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
 // ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
@@ -57,16 +57,16 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
     const int quads = (F + 3) / 4;
     const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + p;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    for (int c0 = 0; c0 < F; c0 += 16) {
-        float xv[16];
+    for (int c0 = 0; c0 < F; c0 += 32) {
+        float xv[32];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < 8; ++g) {
             const f4 v = c0 / 4 + g < quads ? tq[(size_t)(c0 / 4 + g) * A] : f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < 4; ++r) xv[4 * g + r] = v[r];
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < 32; ++u) {
             if (c0 + u < F) {
                 a0 = fmaf(w.convW[c0 + u], xv[u], a0);
                 a1 = fmaf(w.convW[F + c0 + u], xv[u], a1);
@@ -95,6 +95,43 @@ constexpr int kFcOutTile = 64;
 
 __host__ __device__ constexpr int headPad16(int x) { return (x + 15) / 16 * 16; }
 
+// One 16 x 16 block of a head Linear: positions 0..15 (LDS rows of stride
+// RS) x columns n0..n0+15 of W^T [KPAD][ld]. Lane (m, kk) ends holding
+// (position 4*kk + r, column n0 + m). A step is 16 K values: one LDS read
+// and four MFMAs, in K order. Steps go in groups of eight: the group's 32
+// weight loads are issued before its first MFMA, so a group waits for one
+// load round trip instead of eight (one step is far shorter than a load's
+// round trip).
+template <int KPAD, int RS>
+__device__ __forceinline__ f4 fcBlock(const f4* xs4, int m, int kk, int n0, int ld, const float* wt) {
+    constexpr int kGroup = 8;
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+    for (int g0 = 0; g0 < KPAD; g0 += 16 * kGroup) {
+        float bv[kGroup][4];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            const int k0 = g0 + 16 * u;
+            if (k0 < KPAD) {
+                const float* wr = wt + (size_t)(k0 + 4 * kk) * ld + n0 + m;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bv[u][j] = wr[(size_t)j * ld];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            const int k0 = g0 + 16 * u;
+            if (k0 < KPAD) {
+                const f4 av = xs4[(m * RS + k0) / 4 + kk];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[u][j], acc, 0, 0, 0);
+            }
+        }
+    }
+    return acc;
+}
+
 template <int N>
 __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ act, HeadWeights w,
                                                     float* __restrict__ logits, float* __restrict__ values, int B,
@@ -104,8 +141,9 @@ __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ ac
     constexpr int KV = headPad16(A);              // value K, padded
     constexpr int NP = headPad16(A1);             // policy outputs, padded
     constexpr int RS = KP + 4;                    // LDS row stride (floats)
+    constexpr int HS = 257;                       // hidden-row stride: fc2's rows in distinct banks
     __shared__ f4 xs4[kFcBoards * RS / 4];
-    __shared__ float hid[kFcBoards * 256];
+    __shared__ float hid[kFcBoards * HS];
     float* xs = reinterpret_cast<float*>(xs4);
     const int b0 = blockIdx.x * kFcBoards;
     const int nb = min(kFcBoards, B - b0);
@@ -114,31 +152,34 @@ __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ ac
     const bool policy = (int)blockIdx.y < policyTiles;
     const int K = policy ? 2 * A : A, KPad = policy ? KP : KV;
     const int src = policy ? 0 : 2 * A;
-    for (int i = tid; i < kFcBoards * KPad; i += 256) {
-        const int bb = i / KPad, k = i - bb * KPad;
-        xs[bb * RS + k] = (bb < nb && k < K) ? act[(size_t)(b0 + bb) * 3 * A + src + k] : 0.0f;
+    // Stage the rows, eight loads in flight per thread: every load reads a
+    // valid element (act[0] in place of padding), and padding stores zero.
+    constexpr int kStage = 8;
+    const int total = kFcBoards * KPad;
+    for (int i0 = 0; i0 < total; i0 += 256 * kStage) {
+        float v[kStage];
+        bool ok[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = i0 + u * 256 + tid;
+            const int bb = i / KPad, k = i - bb * KPad;
+            ok[u] = i < total && bb < nb && k < K;
+            v[u] = act[ok[u] ? (size_t)(b0 + bb) * 3 * A + src + k : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = i0 + u * 256 + tid;
+            const int bb = i / KPad, k = i - bb * KPad;
+            if (i < total) xs[bb * RS + k] = ok[u] ? v[u] : 0.0f;
+        }
     }
     __syncthreads();
 
     const int m = lane & 15, kk = lane >> 4;
-    // One 16 x 16 block: positions 0..15 x columns n0..n0+15 of W^T [KPad][ld].
-    auto block = [&](int n0, int ld, const float* wt) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k0 = 0; k0 < KPad; k0 += 16) {
-            const f4 av = xs4[(m * RS + k0) / 4 + kk];
-            const float* wr = wt + (size_t)(k0 + 4 * kk) * ld + n0 + m;
-            float bv[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = wr[(size_t)j * ld];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc, 0, 0, 0);
-        }
-        return acc;   // lane holds (position 4*kk + r, column n0 + m)
-    };
     if (policy) {
         const int n0 = blockIdx.y * kFcOutTile + wave * 16;
         if (n0 >= NP) return;
-        const f4 acc = block(n0, NP, w.policyWT);
+        const f4 acc = fcBlock<KP, RS>(xs4, m, kk, n0, NP, w.policyWT);
         const int a = n0 + m;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -149,20 +190,20 @@ __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ ac
     }
     const int VP = headPad16(V);
     for (int n0 = wave * 16; n0 < VP; n0 += 64) {
-        const f4 acc = block(n0, VP, w.fc1WT);
+        const f4 acc = fcBlock<KV, RS>(xs4, m, kk, n0, VP, w.fc1WT);
         const int v = n0 + m;
         if (v < V) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float h = __fadd_rn(acc[r], w.fc1B[v]);
-                hid[(4 * kk + r) * 256 + v] = h > 0.0f ? h : 0.0f;
+                hid[(4 * kk + r) * HS + v] = h > 0.0f ? h : 0.0f;
             }
         }
     }
     __syncthreads();
     if (tid < nb) {
         float s = 0.0f;
-        for (int u = 0; u < V; ++u) s = fmaf(hid[tid * 256 + u], w.fc2W[u], s);
+        for (int u = 0; u < V; ++u) s = fmaf(hid[tid * HS + u], w.fc2W[u], s);
         values[b0 + tid] = tanhf(__fadd_rn(s, w.fc2B[0]));
     }
 }
