@@ -40,8 +40,8 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
 // and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
-// one point per thread, the trunk read in channel quads (eight 16-byte loads
-// per 32 channels) ahead of their FMAs:
+// one point per thread, the trunk read in channel quads (sixteen 16-byte
+// loads per 64 channels) ahead of their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
 // src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
 // ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
@@ -57,16 +57,16 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
     const int quads = (F + 3) / 4;
     const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + p;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    for (int c0 = 0; c0 < F; c0 += 32) {
-        float xv[32];
+    for (int c0 = 0; c0 < F; c0 += 64) {
+        float xv[64];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < 16; ++g) {
             const f4 v = c0 / 4 + g < quads ? tq[(size_t)(c0 / 4 + g) * A] : f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < 4; ++r) xv[4 * g + r] = v[r];
         }
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
+        for (int u = 0; u < 64; ++u) {
             if (c0 + u < F) {
                 a0 = fmaf(w.convW[c0 + u], xv[u], a0);
                 a1 = fmaf(w.convW[F + c0 + u], xv[u], a1);
