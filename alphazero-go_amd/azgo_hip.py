@@ -102,6 +102,7 @@ def load():
             "azh_time_passes": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_time_tower_convs": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int), P(C.c_int)], C.c_int),
             "azh_time_round_trips": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_time_pipelined": ([vp, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    f32], C.c_int),
             "azh_time_conv3x3": ([C.c_int] * 6 + [f32], C.c_int),
@@ -399,6 +400,13 @@ class Runner:
     def time_round_trips(self, slot, B, iters):
         ms = C.c_float()
         _check(self.lib.azh_time_round_trips(self.h, slot, B, iters, C.byref(ms)))
+        return ms.value
+
+    def time_pipelined(self, B, passes):
+        """Wall ms for `passes` passes of B with every slot kept full
+        through begin/done (each slot's input must hold B positions)."""
+        ms = C.c_float()
+        _check(self.lib.azh_time_pipelined(self.h, B, passes, C.byref(ms)))
         return ms.value
 
     # ---- probes

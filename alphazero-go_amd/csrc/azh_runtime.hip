@@ -1342,6 +1342,57 @@ int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms) {
     });
 }
 
+int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms) {
+    return guarded([&] {
+        if (!r || !ms || passes < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        r->checkBatch(B);
+        const int slots = azh_slots(r);
+        for (int i = 0; i < slots; ++i) r->idleSlot(i);
+        // The done handler's state outlives every pass it is handed to: all
+        // of them are drained before this function returns.
+        struct Done {
+            std::mutex m;
+            std::condition_variable cv;
+            std::vector<int> ready;
+            std::string error;
+        } st;
+        const azh_done_fn done = [](void* user, int slot, const char* error) {
+            Done* d = static_cast<Done*>(user);
+            std::lock_guard<std::mutex> lock(d->m);
+            if (error && *error && d->error.empty()) d->error = error;
+            d->ready.push_back(slot);
+            d->cv.notify_one();
+        };
+        int inFlight = 0, begun = 0;
+        auto begin = [&](int slot) {
+            if (azh_begin(r, slot, B, done, &st) != AZH_OK) {
+                std::lock_guard<std::mutex> lock(st.m);
+                if (st.error.empty()) st.error = azh_last_error();
+                return;
+            }
+            ++inFlight;
+            ++begun;
+        };
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < slots && begun < passes; ++i) begin(i);
+        while (inFlight > 0) {
+            int slot;
+            bool failed;
+            {
+                std::unique_lock<std::mutex> lock(st.m);
+                st.cv.wait(lock, [&] { return !st.ready.empty(); });
+                slot = st.ready.back();
+                st.ready.pop_back();
+                failed = !st.error.empty();
+            }
+            --inFlight;
+            if (!failed && begun < passes) begin(slot);
+        }
+        *ms = (float)std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        if (!st.error.empty()) throw Error(AZH_ERR_HIP, st.error);
+    });
+}
+
 int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const float* shift, const float* skip,
                       int relu, int B, int n, int cin, int cout, int tiling, float* y) {
     return guarded([&] {

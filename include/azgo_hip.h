@@ -258,6 +258,16 @@ int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, i
 /* Events around `iters` synchronous round trips: pinned H2D, pass, D2H. */
 int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
 
+/* The runner kept full, as the reference's bench measures its GPU runner
+ * (measureGpuPipelined, apps/bench.cpp:227-279): every slot always has a
+ * pass of B in flight through azh_begin (pinned H2D, pass, D2H, the
+ * completion thread's done), each slot resubmitted as soon as its done
+ * comes, until `passes` passes have completed. Each slot's input must hold
+ * B positions; every slot must be idle. *ms = wall milliseconds from the
+ * first begin to the last done. A pass that fails stops the resubmission;
+ * the passes in flight are drained and the error is returned. */
+int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms);
+
 /* ---------------------------------------------------------------- kernel probes (tests) */
 
 /* The pass's 3x3 convolution kernel alone (cuda_probe::convBnRelu,

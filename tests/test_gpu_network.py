@@ -340,6 +340,33 @@ def test_runner_failure_injection(hip):
         assert results[2] and "injected failure" in results[2]
 
 
+def test_runner_kept_full(hip):
+    """The reference bench's pipelined measurement (apps/bench.cpp:227-279)
+    through begin/done: every pass completes once, each slot's outputs are
+    the synchronous pass's bits, and an injected failure stops the
+    resubmission, drains the passes in flight and is reported."""
+    w = O.WORKLOADS[2]
+    net = O.init_network(w.cfg)
+    inp, _ = O.workload_inputs(w, 64)
+    with _runner(hip, net, 64, slots=2) as r:
+        sync = r.infer(inp[:48])
+        for slot in (0, 1):
+            r.input(slot)[:48] = inp[:48]
+        before = hip.passes_completed()
+        ms = r.time_pipelined(48, 9)
+        assert ms > 0 and hip.passes_completed() - before == 9
+        for slot in (0, 1):
+            assert bitwise_equal(r.logits(slot, 48), sync[0]) and bitwise_equal(r.values(slot, 48), sync[1])
+        hip.fail_passes_after(3)
+        try:
+            with pytest.raises(hip.HipError, match="injected failure"):
+                r.time_pipelined(48, 20)
+        finally:
+            hip.fail_passes_after(0)
+        # Drained: both slots take passes again.
+        assert r.time_pipelined(48, 2) > 0
+
+
 def test_runner_rejects_bad_begin(hip):
     w = O.WORKLOADS[1]
     net = O.init_network(w.cfg)
