@@ -278,6 +278,9 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
                          const float* skip, float* y, int B, int n, int cin, int cout, bool relu, bool planarInput,
                          ConvTiling t, hipStream_t stream) {
+    // A launch needs at least one input channel (one K chunk) and one
+    // output channel: the kernel reads the weights of chunk 0.
+    if (cin < 1 || cout < 1) return hipErrorInvalidValue;
     if (B < 1) return hipSuccess;
     switch (n) {
     case 5: return launchConvN<5>(x, wPacked, scale, shift, skip, y, B, cin, cout, relu, planarInput, t, stream);
