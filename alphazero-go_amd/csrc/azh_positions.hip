@@ -277,6 +277,63 @@ __global__ __launch_bounds__(256) void priorsKernel(const float* __restrict__ lo
     for (int a = lane; a < actions; a += 64) o[a] = m[a] ? expf(logit(a) - mx) / sum : 0.0f;
 }
 
+// The same priors with a lane's actions (a = lane + 64u, u < PER) held in
+// registers: every logit and legal byte is loaded once, all of them before
+// the first reduction, and each exp is computed once. Same arithmetic in
+// the same order as priorsKernel (per-lane partial sums in a ascending,
+// then the same butterfly), so the same bits; for actions <= 64 * PER.
+template <int PER>
+__global__ __launch_bounds__(256) void priorsRegsKernel(const float* __restrict__ logits,
+                                                        const uint8_t* __restrict__ legal,
+                                                        const uint8_t* __restrict__ sym, float* __restrict__ mapped,
+                                                        float* __restrict__ priors, int B, int actions, int n) {
+    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (pos >= B) return;   // a whole wave leaves together
+    const float* l = logits + (size_t)pos * actions;
+    const uint8_t* m = legal + (size_t)pos * actions;
+    float* o = priors + (size_t)pos * actions;
+    const int s = sym ? sym[pos] : 0;
+    const int area = actions - 1;
+    float v[PER];
+    bool ok[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int a = lane + 64 * u;
+        const int at = a < actions ? a : 0;   // lanes past the actions read action 0, unused
+        v[u] = l[(s == 0 || at == area) ? at : transformPoint(s, at, n)];
+        ok[u] = a < actions && m[at] != 0;
+    }
+    if (mapped) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (lane + 64 * u < actions) mapped[(size_t)pos * actions + lane + 64 * u] = v[u];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+        if (ok[u]) mx = fmaxf(mx, v[u]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (mx == -INFINITY) {   // no legal action: nothing to normalise
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (lane + 64 * u < actions) o[lane + 64 * u] = 0.0f;
+        return;
+    }
+    float e[PER];
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        e[u] = ok[u] ? expf(v[u] - mx) : 0.0f;
+        if (ok[u]) sum += e[u];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+        if (lane + 64 * u < actions) o[lane + 64 * u] = ok[u] ? e[u] / sum : 0.0f;
+}
+
 } // namespace
 
 hipError_t launchEncodePlanes(const uint8_t* stones, const int* plies, const uint8_t* toMove, const uint8_t* sym,
@@ -302,8 +359,13 @@ hipError_t launchPriors(const float* logits, const uint8_t* legal, const uint8_t
                         int B, int actions, int n, hipStream_t stream) {
     if (B < 1) return hipSuccess;
     if (sym && actions != n * n + 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(priorsKernel, dim3(ceilDiv(B, 4)), dim3(256), 0, stream, logits, legal, sym, mapped, priors, B,
-                       actions, n);
+    // Up to 384 actions (every board up to 19x19 and its pass) from registers.
+    if (actions <= 64 * 6)
+        hipLaunchKernelGGL(priorsRegsKernel<6>, dim3(ceilDiv(B, 4)), dim3(256), 0, stream, logits, legal, sym, mapped,
+                           priors, B, actions, n);
+    else
+        hipLaunchKernelGGL(priorsKernel, dim3(ceilDiv(B, 4)), dim3(256), 0, stream, logits, legal, sym, mapped, priors,
+                           B, actions, n);
     return hipGetLastError();
 }
 

@@ -288,6 +288,24 @@ def test_softmax_legal_vs_oracle(hip):
     assert got[3, 361] == 1.0
 
 
+def test_softmax_register_and_loop_kernels_agree(hip):
+    """Rows of up to 384 actions take the register kernel, longer ones the
+    loop kernel; with one more action that is illegal both sum the same
+    values in the same order, so the priors are the same bits."""
+    rng = np.random.default_rng(9)
+    B, A = 37, 384
+    logits = (rng.standard_normal((B, A)) * 8).astype(np.float32)
+    legal = (rng.random((B, A)) < 0.6).astype(np.uint8)
+    legal[5, :] = 0   # nothing legal: all zeros
+    regs = hip.softmax_legal(logits, legal)
+    longer = hip.softmax_legal(np.concatenate([logits, np.full((B, 1), 50.0, np.float32)], axis=1),
+                               np.concatenate([legal, np.zeros((B, 1), np.uint8)], axis=1))
+    assert bitwise_equal(regs, longer[:, :A]) and np.all(longer[:, A] == 0)
+    assert np.all(regs[5] == 0)
+    ref = O.softmax_legal(logits, legal)
+    assert np.abs(regs.astype(np.float64) - ref).max() <= 1e-6
+
+
 def test_runner_slots_async(hip):
     """BatchRunner's contract (include/azgo/inference_hub.hpp:41-53): begin on
     each slot returns at once, done comes once per pass from the completion
