@@ -75,10 +75,6 @@ std::atomic<int> gCopyOutDelayUs{0};
 
 // Free memory a check leaves for everything else (src/cuda/cuda_runner.cu:50).
 constexpr size_t kMemoryMargin = size_t(512) << 20;
-// The completion thread's polling interval, first and longest
-// (src/cuda/cuda_runner.cu:47): it sleeps instead of spinning a core that
-// the tree search needs.
-constexpr int kPollFirstUs = 50, kPollLastUs = 200;
 constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
 // The workgroup shapes a probe may force (include/azgo_hip.h lists them).
 const azh::ConvTiling* const kTilings = azh::kConvTilings;
@@ -590,7 +586,11 @@ struct Slot {
     Slot(const Shape& s, int maxBatch) {
         const size_t B = maxBatch;
         check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
-        check(hipEventCreateWithFlags(&event, hipEventDisableTiming), "hipEventCreate");
+        // Blocking sync: the completion thread sleeps in the driver until the
+        // pass's end wakes it, without spinning a core and without the
+        // tens of microseconds a timed sleep overshoots by (on small passes
+        // that overshoot was up to 40% of the runner-kept-full rate).
+        check(hipEventCreateWithFlags(&event, hipEventDisableTiming | hipEventBlockingSync), "hipEventCreate");
         check(hipMalloc(&dev, slotFloats(s, maxBatch) * sizeof(float)), "hipMalloc(workspace)");
         size_t off = 0;
         auto take = [&](size_t f) {
@@ -842,15 +842,7 @@ struct azh_runner {
               "hipMemcpyAsync(values)");
     }
 
-    static hipError_t waitFor(hipEvent_t e) {
-        int sleepUs = kPollFirstUs;
-        for (;;) {
-            const hipError_t r = hipEventQuery(e);
-            if (r != hipErrorNotReady) return r;
-            std::this_thread::sleep_for(std::chrono::microseconds(sleepUs));
-            sleepUs = std::min(kPollLastUs, 2 * sleepUs);
-        }
-    }
+    static hipError_t waitFor(hipEvent_t e) { return hipEventSynchronize(e); }
 
     void completionLoop() {
         for (;;) {
