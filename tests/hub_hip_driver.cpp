@@ -4,7 +4,7 @@
 // scenarios follow the reference's runner and hub tests
 // (tests/test_cuda.cpp:1022-1237, tests/test_inference_hub.cpp:272-628).
 //
-//   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain | ownership
+//   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain | ownership | throughput
 //
 // Prints "PASS <scenario>" and exits 0, or prints what failed and exits 1.
 #include <algorithm>
@@ -316,11 +316,72 @@ void ownership() {
     expect(dLog <= 1e-4 * std::max(1.0, maxLog), "logits within 1e-4 (relative to the largest) of Network::infer");
 }
 
+// The reference bench's hub load (measureHub, apps/bench.cpp:282-307):
+// `workers` threads each sending batch-8 requests of its own random
+// positions in a loop through one hub of inference_batch 256 on this
+// backend's runner (2 slots), for `seconds`. Reports positions per second,
+// the hub's mean pass size and the slots' busy fraction; fails only if an
+// evaluation throws or nothing was evaluated.
+void throughputOf(const NetConfig& cfg, int workers, double seconds) {
+    const Network net(cfg, 1);
+    InferenceHubOptions options;
+    options.maxBatch = 256;
+    InferenceHub hub(makeHipRunner(net, options.maxBatch, 2), cfg, options);
+    std::atomic<bool> stop{false};
+    std::atomic<long long> evals{0};
+    std::atomic<int> errors{0};
+    std::vector<std::thread> threads;
+    const auto start = std::chrono::steady_clock::now();
+    for (int w = 0; w < workers; ++w) {
+        threads.emplace_back([&, w] {
+            try {
+                std::unique_ptr<Evaluator> ev = hub.makeEvaluator(8);
+                Rng rng(static_cast<uint64_t>(100 + w));
+                const std::vector<float> in = randomPositions(cfg, 8, rng);
+                std::vector<float> logits(8 * static_cast<size_t>(cfg.actions())), values(8);
+                long long mine = 0;
+                while (!stop.load(std::memory_order_relaxed)) {
+                    ev->evaluate(in.data(), 8, logits.data(), values.data());
+                    mine += 8;
+                }
+                evals += mine;
+            } catch (const std::exception&) {
+                ++errors;
+                stop = true;
+            }
+        });
+    }
+    while (!stop.load() &&
+           std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count() < seconds)
+        std::this_thread::sleep_for(std::chrono::milliseconds(5));
+    stop = true;
+    for (std::thread& t : threads) t.join();
+    const double elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+    const InferenceHub::Stats st = hub.stats();
+    std::printf("throughput %dx%d %dx%d V=%d: %d workers x batch-8 requests: %.0f positions/s, mean pass %.1f, "
+                "slots busy %.2f\n",
+                cfg.boardSize, cfg.boardSize, cfg.blocks, cfg.filters, cfg.valueHidden, workers,
+                static_cast<double>(evals.load()) / elapsed,
+                st.batches > 0 ? static_cast<double>(st.positions) / static_cast<double>(st.batches) : 0.0,
+                st.gpuSeconds / (elapsed * kInferenceSlots));
+    std::fflush(stdout);
+    expect(errors.load() == 0, "no evaluation failed");
+    expect(evals.load() > 0, "positions were evaluated");
+}
+
+void throughput() {
+    // The reference's 19x19 preset (value head 256), as its published hub
+    // figure is measured (docs/results/cuda-bench.txt:307), and the 9x9
+    // network of the benchmark workloads.
+    throughputOf(config(19, 10, 128, 256), 256, 3.0);
+    throughputOf(config(9, 6, 64, 64), 256, 3.0);
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
     if (argc != 2) {
-        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership\n");
+        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership|throughput\n");
         return 2;
     }
     std::string why;
@@ -336,6 +397,7 @@ int main(int argc, char** argv) {
         else if (s == "refusals") refusals();
         else if (s == "ownership") ownership();
         else if (s == "drain") drain();
+        else if (s == "throughput") throughput();
         else {
             std::printf("unknown scenario %s\n", s.c_str());
             return 2;

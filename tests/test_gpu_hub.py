@@ -12,7 +12,9 @@ injected failure reaching every later
 request, the memory refusal, argument refusals, the destructor draining
 a delayed pass whose outputs are on the host when done comes, and the
 ownership head through HipInference against the reference's own
-Network::infer (naive backend) on a network with the head.
+Network::infer (naive backend) on a network with the head; and the
+reference bench's hub load (256 threads of batch-8 requests, apps/bench.cpp:
+282-307), whose positions per second it prints.
 """
 import os
 import subprocess
@@ -29,7 +31,7 @@ pytestmark = [
 ]
 
 
-@pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain", "ownership"])
+@pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain", "ownership", "throughput"])
 def test_reference_hub_drives_hip_runner(hip, scenario):
     r = subprocess.run([DRIVER, scenario], capture_output=True, text=True, timeout=120)
     print(r.stdout)
