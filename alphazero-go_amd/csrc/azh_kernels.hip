@@ -255,9 +255,8 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     // 5x5 boards at batches 1 to 512:
     // - large layers (the headline 256 boards x 128 channels has 47k tiles):
     //   4 waves of 16 channels over the whole board, 64 channels per
-    //   workgroup, two workgroups resident per CU (226 registers per lane,
-    //   56 KB of LDS each), one hiding the other's staging, barriers and
-    //   epilogue;
+    //   workgroup, two workgroups resident per CU (256 registers per lane,
+    //   56 KB of LDS each), one hiding the other's staging and barriers;
     // - smaller layers spread a board's column groups over waves and
     //   workgroups instead, so a batch of 1 at 128 channels still runs 48
     //   workgroups.
