@@ -59,7 +59,7 @@ def parse():
 def traffic_from_profile(workload_name, kernel_hash, kernel):
     """HBM bytes per launch of the tower convolution, from the committed
     rocprofv3 counter summary of the same kernel and sources, or None."""
-    path = os.path.join(ROOT, "profiles", "conv3x3_tower_hbm_traffic.txt")
+    path = os.path.join(ROOT, "profiles", "conv3x3_tower_19x19_b256_hbm_traffic.txt")
     if not os.path.exists(path):
         return None
     vals = {}
