@@ -102,6 +102,7 @@ def load():
             "azh_time_passes": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_time_tower_convs": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int), P(C.c_int)], C.c_int),
             "azh_time_round_trips": ([vp, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_time_tower_layers": ([vp, C.c_int, C.c_int, C.c_int, f32, P(C.c_int)], C.c_int),
             "azh_time_pipelined": ([vp, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_conv3x3": ([f32, f32, f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    f32], C.c_int),
@@ -396,6 +397,12 @@ class Runner:
         n, layers = C.c_int(), C.c_int()
         _check(self.lib.azh_time_tower_convs(self.h, slot, B, iters, C.byref(ms), C.byref(n), C.byref(layers)))
         return ms.value, n.value, layers.value
+
+    def time_tower_layers(self, slot, B, iters):
+        """(total ms, layers) of `iters` runs of the tower as the pass runs it."""
+        ms, layers = C.c_float(), C.c_int()
+        _check(self.lib.azh_time_tower_layers(self.h, slot, B, iters, C.byref(ms), C.byref(layers)))
+        return ms.value, layers.value
 
     def time_round_trips(self, slot, B, iters):
         ms = C.c_float()

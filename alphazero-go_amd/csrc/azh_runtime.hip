@@ -569,6 +569,10 @@ void checkPositions(const uint8_t* stones, size_t stoneBytes, const int32_t* pli
 struct Slot {
     hipStream_t stream = nullptr;
     hipEvent_t event = nullptr;
+    // A large pass runs as two half-batch chains, the second on `aux`,
+    // forked from and joined back into `stream` (azh_runner::launchPass).
+    hipStream_t aux = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     float* dev = nullptr;
     float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dAct = nullptr, *dLogits = nullptr, *dValues = nullptr;
     float* dOwn = nullptr;   // [B][A] after tanh, only with the ownership head
@@ -591,6 +595,9 @@ struct Slot {
         // tens of microseconds a timed sleep overshoots by (on small passes
         // that overshoot was up to 40% of the runner-kept-full rate).
         check(hipEventCreateWithFlags(&event, hipEventDisableTiming | hipEventBlockingSync), "hipEventCreate");
+        check(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking), "hipStreamCreate");
+        check(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "hipEventCreate");
+        check(hipEventCreateWithFlags(&join, hipEventDisableTiming), "hipEventCreate");
         check(hipMalloc(&dev, slotFloats(s, maxBatch) * sizeof(float)), "hipMalloc(workspace)");
         size_t off = 0;
         auto take = [&](size_t f) {
@@ -612,8 +619,12 @@ struct Slot {
     }
     ~Slot() {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (aux) (void)hipStreamSynchronize(aux);
         for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
         if (event) (void)hipEventDestroy(event);
+        if (fork) (void)hipEventDestroy(fork);
+        if (join) (void)hipEventDestroy(join);
+        if (aux) (void)hipStreamDestroy(aux);
         if (stream) (void)hipStreamDestroy(stream);
         if (dev) (void)hipFree(dev);
         if (hIn) (void)hipHostFree(hIn);
@@ -701,39 +712,93 @@ struct azh_runner {
         slots.clear();
     }
 
-    // The pass's kernels on `stream`: stem, `blocksToRun` residual blocks
-    // (the trunk updated in place: the second conv's epilogue reads the skip
-    // at exactly the element it writes), then the heads when asked.
-    // The residual tower's first `blocksToRun` blocks on slot s's trunk.
-    // Returns the number of launches.
-    int launchTower(Slot& s, int B, hipStream_t stream, int blocksToRun) {
+    // The residual tower's first `blocksToRun` blocks on a trunk of Bp
+    // boards (x in place; mid, the blocks' middle activations), workgroup
+    // shape t, on `stream`: each block's second convolution reads the skip
+    // at exactly the element it writes. Returns the number of launches.
+    int launchTowerOn(float* x, float* mid, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun) {
         const Shape& sh = shape;
-        if (blocksToRun < 1) return 0;
-        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
         for (int i = 0; i < blocksToRun; ++i) {
             const ConvW& a = weights.conv1[i];
             const ConvW& b = weights.conv2[i];
-            check(azh::launchConv3x3(s.dX, a.w, a.scale, a.shift, nullptr, s.dMid, B, sh.n, sh.F, sh.F, true, false,
-                                     t, stream),
+            check(azh::launchConv3x3(x, a.w, a.scale, a.shift, nullptr, mid, Bp, sh.n, sh.F, sh.F, true, false, t,
+                                     stream),
                   "conv3x3 (conv1)");
-            check(azh::launchConv3x3(s.dMid, b.w, b.scale, b.shift, s.dX, s.dX, B, sh.n, sh.F, sh.F, true, false,
-                                     t, stream),
+            check(azh::launchConv3x3(mid, b.w, b.scale, b.shift, x, x, Bp, sh.n, sh.F, sh.F, true, false, t, stream),
                   "conv3x3 (conv2)");
         }
-        return 2 * blocksToRun;
+        return 2 * std::max(blocksToRun, 0);
     }
 
-    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+    // The residual tower over slot s's whole batch on one stream, every
+    // launch over all B boards (the tower kernel as timed on its own).
+    int launchTower(Slot& s, int B, hipStream_t stream, int blocksToRun) {
+        return launchTowerOn(s.dX, s.dMid, B, azh::chooseConvTiling(shape.F, B, shape.n), stream, blocksToRun);
+    }
+
+    // Boards [b0, b0 + Bp) of slot s's pass on `stream`: the stem,
+    // `blocksToRun` residual blocks, then the heads when asked; workgroup
+    // shape t (the shape decides only which workgroup computes an output,
+    // never how, so a part's bits are the whole batch's).
+    void launchPassPart(Slot& s, int b0, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun,
+                        bool heads) {
         const Shape& sh = shape;
-        const azh::ConvTiling t = azh::chooseConvTiling(sh.F, B, sh.n);
-        check(azh::launchConv3x3(s.dIn, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, s.dX, B,
-                                 sh.n, sh.P, sh.F, true, true, t, stream),
+        const size_t trunk = azh::quadFloats(1, sh.F, sh.A);   // floats per board
+        float* x = s.dX + b0 * trunk;
+        float* mid = s.dMid + b0 * trunk;
+        check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
+                                 weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
               "conv3x3 (stem)");
-        launchTower(s, B, stream, blocksToRun);
+        launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
         if (heads)
-            check(azh::launchHeads(s.dX, weights.heads, s.dAct, s.dLogits, s.dValues, s.dOwn, B, sh.n, sh.F, sh.V,
-                                   stream),
+            check(azh::launchHeads(x, weights.heads, s.dAct + (size_t)b0 * 3 * sh.A, s.dLogits + (size_t)b0 * sh.A1,
+                                   s.dValues + b0, s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr, Bp, sh.n, sh.F,
+                                   sh.V, stream),
                   "heads");
+    }
+
+    // Whether a pass of B runs as two half-batch chains on two streams. With
+    // the whole-board workgroup shapes (the large batches) a layer is one
+    // round of workgroups that all start and end together: its launch and
+    // its epilogue's output burst leave the matrix units idle. Two
+    // independent halves on two streams drift apart, so one half's layer
+    // tail overlaps the other's contraction (19x19 10x128: 197.9 -> 193.1 us
+    // per layer of 256 boards, 391.6 -> 382.9 us at 512; four quarters were
+    // slower than one stream).
+    bool splitPass(int B) const { return B >= 2 && azh::chooseConvTiling(shape.F, B, shape.n).pgPerWave == 0; }
+
+    // The pass's kernels, issued on `stream` (slot s's own or its capture):
+    // the whole batch, or for a large batch its two halves, the second on
+    // s.aux, forked from `stream` and joined back into it.
+    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+        if (!splitPass(B)) {
+            launchPassPart(s, 0, B, t, stream, blocksToRun, heads);
+            return;
+        }
+        const int B0 = (B + 1) / 2;
+        check(hipEventRecord(s.fork, stream), "hipEventRecord(fork)");
+        check(hipStreamWaitEvent(s.aux, s.fork, 0), "hipStreamWaitEvent(fork)");
+        launchPassPart(s, 0, B0, t, stream, blocksToRun, heads);
+        launchPassPart(s, B0, B - B0, t, s.aux, blocksToRun, heads);
+        check(hipEventRecord(s.join, s.aux), "hipEventRecord(join)");
+        check(hipStreamWaitEvent(stream, s.join, 0), "hipStreamWaitEvent(join)");
+    }
+
+    // The tower as the pass runs it (two half-batch chains for a large
+    // batch), on slot s's staged trunk: the effective time per layer.
+    int launchTowerAsPass(Slot& s, int B, int blocksToRun) {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+        if (!splitPass(B)) return launchTowerOn(s.dX, s.dMid, B, t, s.stream, blocksToRun);
+        const int B0 = (B + 1) / 2;
+        const size_t trunk = azh::quadFloats(1, shape.F, shape.A);
+        check(hipEventRecord(s.fork, s.stream), "hipEventRecord(fork)");
+        check(hipStreamWaitEvent(s.aux, s.fork, 0), "hipStreamWaitEvent(fork)");
+        int n = launchTowerOn(s.dX, s.dMid, B0, t, s.stream, blocksToRun);
+        n += launchTowerOn(s.dX + B0 * trunk, s.dMid + B0 * trunk, B - B0, t, s.aux, blocksToRun);
+        check(hipEventRecord(s.join, s.aux), "hipEventRecord(join)");
+        check(hipStreamWaitEvent(s.stream, s.join, 0), "hipStreamWaitEvent(join)");
+        return n;
     }
 
     // The device-resident pass: one captured graph per batch size, replayed.
@@ -1314,6 +1379,17 @@ int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, i
         int per = 0;
         *ms = timeOnStream(s.stream, iters, [&] { per = r->launchTower(s, B, s.stream, r->shape.blocks); });
         *launches = iters * per;
+        *layers = iters * 2 * r->shape.blocks;
+    });
+}
+
+int azh_time_tower_layers(azh_runner* r, int slot, int B, int iters, float* ms, int* layers) {
+    return guarded([&] {
+        if (!r || !ms || !layers || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
+        r->checkBatch(B);
+        Slot& s = r->idleSlot(slot);
+        *ms = timeOnStream(s.stream, iters, [&] { r->launchTowerAsPass(s, B, r->shape.blocks); });
         *layers = iters * 2 * r->shape.blocks;
     });
 }

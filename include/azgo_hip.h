@@ -255,6 +255,13 @@ int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms);
  * number of layers they ran, for the dominant kernel's average launch time. */
 int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches, int* layers);
 
+/* HIP events on the slot's stream around `iters` runs of the residual
+ * tower as the pass runs it: one stream, or for a large batch two
+ * half-batch chains on the slot's two streams, forked from and joined back
+ * into its stream. Total ms and the number of layers (of the whole batch)
+ * run: the tower's effective time per layer within a pass. */
+int azh_time_tower_layers(azh_runner* r, int slot, int B, int iters, float* ms, int* layers);
+
 /* Events around `iters` synchronous round trips: pinned H2D, pass, D2H. */
 int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
 
