@@ -764,8 +764,15 @@ struct azh_runner {
     // independent halves on two streams drift apart, so one half's layer
     // tail overlaps the other's contraction (19x19 10x128: 197.9 -> 193.1 us
     // per layer of 256 boards, 391.6 -> 382.9 us at 512; four quarters were
-    // slower than one stream).
-    bool splitPass(int B) const { return B >= 2 && azh::chooseConvTiling(shape.F, B, shape.n).pgPerWave == 0; }
+    // slower than one stream). The same holds for the four-wave shape of
+    // 6 column groups once a half still has work for every CU (59.4 -> 57.1
+    // us at 64 boards, 116.6 -> 112.7 at 128), not below (at 16 and 32
+    // boards, latency-bound, two halves took 25% longer).
+    bool splitPass(int B) const {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+        const long tiles = (long)B * azh::ceilDiv(shape.F, azh::kCoBlock) * azh::ceilDiv(shape.A, 16);
+        return B >= 2 && (t.pgPerWave == 0 || (t == azh::ConvTiling{1, 1, 4, 6} && tiles >= 10000));
+    }
 
     // The pass's kernels, issued on `stream` (slot s's own or its capture):
     // the whole batch, or for a large batch its two halves, the second on

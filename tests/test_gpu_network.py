@@ -133,25 +133,27 @@ def test_headline_batch_independent(hip):
             assert bitwise_equal(part[0], whole[0][picks]) and bitwise_equal(part[1], whole[1][picks])
 
 
-def test_split_pass_equals_whole(hip):
+@pytest.mark.parametrize("B", [257, 75])
+def test_split_pass_equals_whole(hip, B):
     """A large batch runs as two half-batch chains on two streams (forked
-    and joined inside the captured graph): an odd batch of 257, captured and
-    eager, gives every row the bits of the position alone, on both sides of
-    the split."""
+    and joined inside the captured graph): an odd batch (257: whole-board
+    workgroups; 75: the four-wave shape), captured and eager, gives every
+    row the bits of the position alone, on both sides of the split."""
     w = O.WORKLOADS[3]
     net = O.random_network(w.cfg, 605)
-    inp, _ = O.workload_inputs(w, 257)
-    with _runner(hip, net, 257) as r:
+    inp, _ = O.workload_inputs(w, B)
+    half = (B + 1) // 2
+    with _runner(hip, net, B) as r:
         graph = r.infer(inp)
         again = r.infer(inp)
         assert bitwise_equal(again[0], graph[0]) and bitwise_equal(again[1], graph[1])
-        for s in (0, 127, 128, 129, 130, 256):
+        for s in (0, half - 2, half - 1, half, half + 1, B - 1):
             alone = r.infer(inp[s:s + 1])
             assert bitwise_equal(alone[0][0], graph[0][s]) and bitwise_equal(alone[1][0], graph[1][s])
         r.set_graphs(False)
         eager = r.infer(inp)
         assert bitwise_equal(eager[0], graph[0]) and bitwise_equal(eager[1], graph[1])
-        ms, layers = r.time_tower_layers(0, 257, 1)
+        ms, layers = r.time_tower_layers(0, B, 1)
         assert ms > 0 and layers == 2 * w.cfg.blocks
 
 
