@@ -774,38 +774,40 @@ struct azh_runner {
         return B >= 2 && (t.pgPerWave == 0 || (t == azh::ConvTiling{1, 1, 4, 6} && tiles >= 10000));
     }
 
-    // The pass's kernels, issued on `stream` (slot s's own or its capture):
-    // the whole batch, or for a large batch its two halves, the second on
-    // s.aux, forked from `stream` and joined back into it.
-    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
-        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+    // Runs part(b0, Bp, stream) over slot s's batch of B on `stream` (slot
+    // s's own or its capture): the whole batch, or when the pass splits, its
+    // two halves, the second on s.aux, forked from `stream` and joined back
+    // into it.
+    template <typename Part>
+    void overHalves(Slot& s, int B, hipStream_t stream, Part part) {
         if (!splitPass(B)) {
-            launchPassPart(s, 0, B, t, stream, blocksToRun, heads);
+            part(0, B, stream);
             return;
         }
         const int B0 = (B + 1) / 2;
         check(hipEventRecord(s.fork, stream), "hipEventRecord(fork)");
         check(hipStreamWaitEvent(s.aux, s.fork, 0), "hipStreamWaitEvent(fork)");
-        launchPassPart(s, 0, B0, t, stream, blocksToRun, heads);
-        launchPassPart(s, B0, B - B0, t, s.aux, blocksToRun, heads);
+        part(0, B0, stream);
+        part(B0, B - B0, s.aux);
         check(hipEventRecord(s.join, s.aux), "hipEventRecord(join)");
         check(hipStreamWaitEvent(stream, s.join, 0), "hipStreamWaitEvent(join)");
     }
 
-    // The tower as the pass runs it (two half-batch chains for a large
-    // batch), on slot s's staged trunk: the effective time per layer.
-    int launchTowerAsPass(Slot& s, int B, int blocksToRun) {
+    // The pass's kernels, on `stream`, in halves when the pass splits.
+    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
         const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
-        if (!splitPass(B)) return launchTowerOn(s.dX, s.dMid, B, t, s.stream, blocksToRun);
-        const int B0 = (B + 1) / 2;
+        overHalves(s, B, stream,
+                   [&](int b0, int Bp, hipStream_t st) { launchPassPart(s, b0, Bp, t, st, blocksToRun, heads); });
+    }
+
+    // The tower as the pass runs it, on slot s's staged trunk (the effective
+    // time per layer within a pass).
+    void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
         const size_t trunk = azh::quadFloats(1, shape.F, shape.A);
-        check(hipEventRecord(s.fork, s.stream), "hipEventRecord(fork)");
-        check(hipStreamWaitEvent(s.aux, s.fork, 0), "hipStreamWaitEvent(fork)");
-        int n = launchTowerOn(s.dX, s.dMid, B0, t, s.stream, blocksToRun);
-        n += launchTowerOn(s.dX + B0 * trunk, s.dMid + B0 * trunk, B - B0, t, s.aux, blocksToRun);
-        check(hipEventRecord(s.join, s.aux), "hipEventRecord(join)");
-        check(hipStreamWaitEvent(s.stream, s.join, 0), "hipStreamWaitEvent(join)");
-        return n;
+        overHalves(s, B, s.stream, [&](int b0, int Bp, hipStream_t st) {
+            launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, t, st, blocksToRun);
+        });
     }
 
     // The device-resident pass: one captured graph per batch size, replayed.
