@@ -35,6 +35,9 @@ struct HeadWeights {
 };
 size_t headPolicyWTFloats(int n);
 size_t headFc1WTFloats(int n, int V);
+// Compute units of the current device (cached; 256 if the query fails).
+int deviceCUs();
+
 // The heads on a trunk of F channels in channel quads (azh_conv_iface.hpp).
 hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values,
                        float* own, int B, int n, int F, int V, hipStream_t stream);

@@ -758,20 +758,28 @@ struct azh_runner {
     }
 
     // Whether a pass of B runs as two half-batch chains on two streams. With
-    // the whole-board workgroup shapes (the large batches) a layer is one
+    // the whole-board workgroup shapes (the large batches) a layer is a
     // round of workgroups that all start and end together: its launch and
     // its epilogue's output burst leave the matrix units idle. Two
     // independent halves on two streams drift apart, so one half's layer
     // tail overlaps the other's contraction (19x19 10x128: 197.9 -> 193.1 us
     // per layer of 256 boards, 391.6 -> 382.9 us at 512; four quarters were
-    // slower than one stream). The same holds for the four-wave shape of
-    // 6 column groups once a half still has work for every CU (59.4 -> 57.1
-    // us at 64 boards, 116.6 -> 112.7 at 128), not below (at 16 and 32
-    // boards, latency-bound, two halves took 25% longer).
+    // slower than one stream). Not when the whole batch is a single round
+    // of one workgroup per CU (128 boards: 104.8 us on one stream, 135 in
+    // halves). The same holds for the four-wave shape of 6 column groups
+    // once a half still has work for every CU (59.4 -> 57.1 us at 64
+    // boards, 116.6 -> 112.7 at 128), not below (at 16 and 32 boards,
+    // latency-bound, two halves took 25% longer).
     bool splitPass(int B) const {
+        if (B < 2) return false;
         const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
-        const long tiles = (long)B * azh::ceilDiv(shape.F, azh::kCoBlock) * azh::ceilDiv(shape.A, 16);
-        return B >= 2 && (t.pgPerWave == 0 || (t == azh::ConvTiling{1, 1, 4, 6} && tiles >= 10000));
+        const int coBlocks = azh::ceilDiv(shape.F, azh::kCoBlock);
+        if (t.pgPerWave == 0) {
+            const long workgroups = (long)B * azh::ceilDiv(coBlocks, t.coTile() / azh::kCoBlock);
+            return 2 * workgroups >= 3L * azh::deviceCUs();
+        }
+        const long tiles = (long)B * coBlocks * azh::ceilDiv(shape.A, 16);
+        return t == azh::ConvTiling{1, 1, 4, 6} && tiles >= 10000;
     }
 
     // Runs part(b0, Bp, stream) over slot s's batch of B on `stream` (slot
