@@ -277,7 +277,8 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     //   the widest channel tile that gets there. At 19x19 a board's
     //   workgroup is long enough that a part-filled round of them costs a
     //   whole one, so they wait for about 40k output tiles (one full round
-    //   at 128 channels from 218 boards).
+    //   at 128 channels from 218 boards), or for a batch that gives each
+    //   CU one workgroup.
     // - Smaller layers spread a board's column groups over waves and
     //   workgroups instead, so a batch of 1 at 128 channels still runs 48
     //   workgroups at 19x19.
@@ -285,6 +286,12 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     const int groups = ceilDiv(boardSize * boardSize, 16);
     const long tiles = (long)B * coBlocks * groups;
     if (boardSize >= 19) {
+        // One round of one 4-wave workgroup per CU, or nearly: the
+        // whole-board shape (128 boards at 128 channels: 104.8 us per layer
+        // against 114 for the next best).
+        const long wholeWorkgroups = (long)B * ceilDiv(coBlocks, 4);
+        if (coBlocks >= 4 && wholeWorkgroups <= deviceCUs() && 10 * wholeWorkgroups >= 9L * deviceCUs())
+            return {1, 4, 1, 0};
         if (tiles >= 40000) {
             if (coBlocks >= 4) return {1, 4, 1, 0};
             if (coBlocks >= 2) return {1, 2, 1, 0};
