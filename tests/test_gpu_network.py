@@ -8,6 +8,7 @@ the CPU backends' own gap (tests/test_cuda.cpp:804-849), and argmax agreement
 over legal moves (>= 99.9%). Full-size batches are checked through
 properties: batch independence and repeatability, bit for bit.
 """
+import os
 import threading
 
 import numpy as np
@@ -291,6 +292,60 @@ def test_ownership_heads_probe_vs_double(hip):
     scale = t["ownership.bn.gamma"][0] / np.sqrt(t["ownership.bn.runVar"][0] + np.float64(np.float32(1e-5)))
     ref = np.tanh((conv - t["ownership.bn.runMean"][0]) * scale + t["ownership.bn.beta"][0])
     assert float(np.abs(own - ref).max()) <= 1e-5
+
+
+def test_tanh_within_two_ulp(hip):
+    """The heads' tanh (value and ownership, tanhf) within 2 ulp of tanh in
+    double (tests/test_cuda.cpp:494-512). The ownership head is made to pass
+    a trunk value straight through: 1x1 weights selecting channel 0 (the
+    other channels' terms add exact zeros), BN with gamma 1, beta 0, mean 0
+    and a variance whose float sum with eps is exactly 1."""
+    cfg = O.make_cfg(9, 1, 16, ownership=1)
+    net = O.random_network(cfg, 85)
+    t = net.tensors()
+    t["ownership.conv.w"][:] = 0.0
+    t["ownership.conv.w"][0] = 1.0
+    t["ownership.bn.gamma"][:] = 1.0
+    t["ownership.bn.beta"][:] = 0.0
+    t["ownership.bn.runMean"][:] = 0.0
+    t["ownership.bn.runVar"][:] = np.float32(0.99999)
+    assert np.float32(0.99999) + np.float32(1e-5) == np.float32(1.0)
+    B = 8
+    rng = np.random.default_rng(86)
+    trunk = rng.uniform(-1, 1, (B, 16, 81)).astype(np.float32)
+    x = np.concatenate([np.linspace(-9.5, 9.5, 400), rng.uniform(-3, 3, 200),
+                        [1e-7, -1e-7, 1e-20, 3e-4, -3e-4, 0.5493, 0.881, 20.0, -20.0, 1e-3, 0.1, -0.1, 2.0, 5.0,
+                         8.6, 9.1, 0.03, 0.7, -0.7, 1.5, 4.0, 0.25, 0.125, 0.0625, 1.0, -1.0, 3.0, 0.9]]).astype(np.float32)
+    x = x[:B * 81]
+    x = np.concatenate([x, np.full(B * 81 - len(x), 0.375, np.float32)])
+    trunk[:, 0, :] = x.reshape(B, 81)
+    with hip.Runner(to_hip_cfg(hip, cfg), t, B, 1) as r:
+        _, _, own = r.probe_heads(trunk, ownership=True)
+    ref = np.tanh(x.astype(np.float64))
+    got = own.reshape(-1).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    err = np.abs(got - ref) / ulp
+    assert float(err.max()) <= 2.0, (float(err.max()), float(x[np.argmax(err)]))
+
+
+def test_runner_threads_released(hip):
+    """No thread outlives its runner (tests/test_cuda.cpp:1220-1237): the
+    process's thread count after creating, using and destroying runners of
+    one and two slots is what it was before."""
+    w = O.WORKLOADS[1]
+    net = O.init_network(w.cfg)
+    inp, _ = O.workload_inputs(w, 8)
+    count = lambda: len(os.listdir("/proc/self/task"))
+    with _runner(hip, net, 8, slots=2) as r:   # the HIP runtime's own threads start here
+        r.infer(inp)
+    before = count()
+    for slots in (1, 2, 1, 2):
+        with _runner(hip, net, 8, slots=slots) as r:
+            r.infer(inp)
+            for s in range(slots):
+                r.input(s)[:8] = inp
+            r.time_pipelined(8, 6)
+    assert count() == before
 
 
 def test_softmax_legal_vs_oracle(hip):
