@@ -158,6 +158,36 @@ def test_split_pass_equals_whole(hip, B):
         assert ms > 0 and layers == 2 * w.cfg.blocks
 
 
+def test_every_batch_size_equals_singles(hip):
+    """A runner at every batch size from 1 to 64 (tests/test_cuda.cpp:
+    1022-1069 runs all of them): each size its own graph and workgroup
+    shape, every row the bits of its position alone."""
+    w = O.WORKLOADS[1]
+    net = O.random_network(w.cfg, 606)
+    inp, _ = O.workload_inputs(w, 64)
+    with _runner(hip, net, 64, slots=2) as r:
+        alone = [r.infer(inp[i:i + 1]) for i in range(64)]
+        for B in range(1, 65):
+            got = r.infer(inp[:B])
+            for i in range(B):
+                assert bitwise_equal(got[0][i], alone[i][0][0]) and bitwise_equal(got[1][i], alone[i][1][0]), (B, i)
+
+
+@pytest.mark.parametrize("B", [54, 55, 115, 116, 128, 129, 217, 218])
+def test_shape_and_split_boundaries(hip, B):
+    """19x19 10x128 on both sides of each change of workgroup shape or of
+    the two-chain split: rows at the start, the middle and the end are the
+    bits of their positions alone."""
+    w = O.WORKLOADS[3]
+    net = O.random_network(w.cfg, 607)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B) as r:
+        whole = r.infer(inp)
+        for s in (0, (B - 1) // 2, (B + 1) // 2, B - 1):
+            alone = r.infer(inp[s:s + 1])
+            assert bitwise_equal(alone[0][0], whole[0][s]) and bitwise_equal(alone[1][0], whole[1][s]), s
+
+
 def test_repeatable_and_graph_equals_eager(hip):
     w = O.WORKLOADS[2]
     net = O.random_network(w.cfg, 604)
