@@ -263,6 +263,12 @@ int deviceCUs() {
     return cus;
 }
 
+long convWorkgroups(ConvTiling t, int cout, int B, int boardSize) {
+    const int groups = ceilDiv(boardSize * boardSize, 16);
+    const int groupsPerWorkgroup = t.wavesPg * (t.pgPerWave == 0 ? groups : t.pgPerWave);
+    return (long)B * ceilDiv(cout, t.coTile()) * ceilDiv(groups, groupsPerWorkgroup);
+}
+
 ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     // From a sweep of every shape over boards 5, 9, 13, 19, 32 to 256
     // channels and batches of 1 to 512 on the MI355X (256 CUs); the rule

@@ -37,6 +37,9 @@ size_t headPolicyWTFloats(int n);
 size_t headFc1WTFloats(int n, int V);
 // Compute units of the current device (cached; 256 if the query fails).
 int deviceCUs();
+// Workgroups of one convolution launch of shape t over B boards of
+// boardSize x boardSize with cout output channels (the launcher's grid).
+long convWorkgroups(ConvTiling t, int cout, int B, int boardSize);
 
 // The heads on a trunk of F channels in channel quads (azh_conv_iface.hpp).
 hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, float* logits, float* values,

@@ -757,29 +757,45 @@ struct azh_runner {
                   "heads");
     }
 
-    // Whether a pass of B runs as two half-batch chains on two streams. With
-    // the whole-board workgroup shapes (the large batches) a layer is a
-    // round of workgroups that all start and end together: its launch and
-    // its epilogue's output burst leave the matrix units idle. Two
-    // independent halves on two streams drift apart, so one half's layer
-    // tail overlaps the other's contraction (19x19 10x128: 197.9 -> 193.1 us
-    // per layer of 256 boards, 391.6 -> 382.9 us at 512; four quarters were
-    // slower than one stream). Not when the whole batch is a single round
-    // of one workgroup per CU (128 boards: 104.8 us on one stream, 135 in
-    // halves). The same holds for the four-wave shape of 6 column groups
-    // once a half still has work for every CU (59.4 -> 57.1 us at 64
-    // boards, 116.6 -> 112.7 at 128), not below (at 16 and 32 boards,
-    // latency-bound, two halves took 25% longer).
+    // Whether a pass of B runs as two half-batch chains on two streams.
+    // - Whole-board shapes with more than one round of workgroups (more than
+    //   one per CU): two independent halves drift apart, so one half's
+    //   partly filled last round, its launches and its epilogue's output
+    //   bursts overlap the other half's contraction (19x19 10x128: 197.9 ->
+    //   193.1 us per layer of 256 boards, 391.6 -> 382.9 us at 512). Not at
+    //   one round (128 boards at 19x19: 104.8 us on one stream, 135 in
+    //   halves).
+    // - The four-wave shape of 6 column groups past one round, or at up to
+    //   7/8 of one: there each half takes its own batch's finer shape, so
+    //   the halves together run more workgroups (19x19 10x128, 18 boards:
+    //   34.4 -> 26.2 us per layer, 24.4k -> 32.5k positions/s).
+    // - The smaller shapes past two rounds (9x9 6x64, 140 boards: 19.6 ->
+    //   17.2 us per layer, 517k -> 577k positions/s). Not below: their
+    //   layers take 7-46 us, where a second chain's launches and heads cost
+    //   what the overlap gains, and with two passes in flight on a runner's
+    //   two slots the four chains lose (9x9 6x64, 100 boards: -4% alone,
+    //   -18% with two slots; 19x19 20x256, 8 boards: +7% alone, -19% with
+    //   two slots).
     bool splitPass(int B) const {
         if (B < 2) return false;
         const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
-        const int coBlocks = azh::ceilDiv(shape.F, azh::kCoBlock);
-        if (t.pgPerWave == 0) {
-            const long workgroups = (long)B * azh::ceilDiv(coBlocks, t.coTile() / azh::kCoBlock);
-            return 2 * workgroups >= 3L * azh::deviceCUs();
-        }
-        const long tiles = (long)B * coBlocks * azh::ceilDiv(shape.A, 16);
-        return t == azh::ConvTiling{1, 1, 4, 6} && tiles >= 10000;
+        const long workgroups = azh::convWorkgroups(t, shape.F, B, shape.n);
+        const long cus = azh::deviceCUs();
+        if (t.pgPerWave == 0) return workgroups > cus;
+        if (t == azh::ConvTiling{1, 1, 4, 6}) return workgroups > cus || 8 * workgroups <= 7 * cus;
+        return workgroups > 2 * cus;
+    }
+
+    // The workgroup shape of a part of Bp boards of a pass of B: the batch's
+    // whole-board shape for both halves (the halves of a large batch), else
+    // the part's own batch's shape unless that is a whole-board one (a
+    // 19x19 half of 120 boards at 96 channels would take the one-round
+    // shape: 141.7 us per layer in halves, 122.1 with the batch's shape).
+    azh::ConvTiling partTiling(int B, int Bp) const {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+        if (t.pgPerWave == 0 || Bp == B) return t;
+        const azh::ConvTiling own = azh::chooseConvTiling(shape.F, Bp, shape.n);
+        return own.pgPerWave == 0 ? t : own;
     }
 
     // Runs part(b0, Bp, stream) over slot s's batch of B on `stream` (slot
@@ -803,18 +819,17 @@ struct azh_runner {
 
     // The pass's kernels, on `stream`, in halves when the pass splits.
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
-        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
-        overHalves(s, B, stream,
-                   [&](int b0, int Bp, hipStream_t st) { launchPassPart(s, b0, Bp, t, st, blocksToRun, heads); });
+        overHalves(s, B, stream, [&](int b0, int Bp, hipStream_t st) {
+            launchPassPart(s, b0, Bp, partTiling(B, Bp), st, blocksToRun, heads);
+        });
     }
 
     // The tower as the pass runs it, on slot s's staged trunk (the effective
     // time per layer within a pass).
     void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
-        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
         const size_t trunk = azh::quadFloats(1, shape.F, shape.A);
         overHalves(s, B, s.stream, [&](int b0, int Bp, hipStream_t st) {
-            launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, t, st, blocksToRun);
+            launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, partTiling(B, Bp), st, blocksToRun);
         });
     }
 

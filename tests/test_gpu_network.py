@@ -134,12 +134,15 @@ def test_headline_batch_independent(hip):
             assert bitwise_equal(part[0], whole[0][picks]) and bitwise_equal(part[1], whole[1][picks])
 
 
-@pytest.mark.parametrize("B", [257, 75])
+@pytest.mark.parametrize("B", [257, 75, 21, 17])
 def test_split_pass_equals_whole(hip, B):
-    """A large batch runs as two half-batch chains on two streams (forked
-    and joined inside the captured graph): an odd batch (257: whole-board
-    workgroups; 75: the four-wave shape), captured and eager, gives every
-    row the bits of the position alone, on both sides of the split."""
+    """A batch with more than a round of workgroups, or a small one in the
+    four-wave shape of 6 column groups, runs as two half-batch chains on two
+    streams (forked and joined inside the captured graph), each half in its
+    own batch's shape: an odd batch (257: whole-board workgroups; 75: the
+    four-wave shape; 21: halves of 11 and 10 in a 2-group shape; 17: halves
+    of 9 and 8 in two different shapes), captured and eager, gives every row
+    the bits of the position alone, on both sides of the split."""
     w = O.WORKLOADS[3]
     net = O.random_network(w.cfg, 605)
     inp, _ = O.workload_inputs(w, B)
@@ -173,13 +176,31 @@ def test_every_batch_size_equals_singles(hip):
                 assert bitwise_equal(got[0][i], alone[i][0][0]) and bitwise_equal(got[1][i], alone[i][1][0]), (B, i)
 
 
-@pytest.mark.parametrize("B", [54, 55, 115, 116, 128, 129, 217, 218])
+@pytest.mark.parametrize("B", [5, 6, 8, 9, 16, 17, 18, 28, 29, 32, 33, 34, 115, 116, 128, 129, 217, 218])
 def test_shape_and_split_boundaries(hip, B):
-    """19x19 10x128 on both sides of each change of workgroup shape or of
-    the two-chain split: rows at the start, the middle and the end are the
+    """19x19 10x128 on both sides of each change of workgroup shape, of the
+    two-chain split and of the halves' own shapes (17: halves of 9 and 8
+    boards in two different shapes; 17-28 and 33: halves in a finer shape
+    than the batch's): rows at the start, the middle and the end are the
     bits of their positions alone."""
     w = O.WORKLOADS[3]
     net = O.random_network(w.cfg, 607)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B) as r:
+        whole = r.infer(inp)
+        for s in (0, (B - 1) // 2, (B + 1) // 2, B - 1):
+            alone = r.infer(inp[s:s + 1])
+            assert bitwise_equal(alone[0][0], whole[0][s]) and bitwise_equal(alone[1][0], whole[1][s]), s
+
+
+@pytest.mark.parametrize("B", [128, 129, 191, 192])
+def test_small_shape_split_boundaries(hip, B):
+    """9x9 6x64 around the smaller shapes' split (two chains past two rounds
+    of workgroups, from 129 boards) and the change to whole-board
+    workgroups at 192 boards (one chain again): rows on both sides of the
+    halves are the bits of their positions alone."""
+    w = O.WORKLOADS[2]
+    net = O.random_network(w.cfg, 608)
     inp, _ = O.workload_inputs(w, B)
     with _runner(hip, net, B) as r:
         whole = r.infer(inp)
