@@ -2,7 +2,8 @@
 
 A step is one forward pass of the network over one batch of synthetic
 positions already resident in HBM (the pass replayed as its captured
-hipGraph; a large batch runs as two half-batch chains on the slot's two
+hipGraph; a batch that would leave part of a round of workgroups idle,
+the headline one included, runs as two half-batch chains on the slot's two
 streams, forked and joined inside the graph). Default workload: 19x19, 10
 residual blocks of 128 filters, batch 256 (the headline configuration).
 Prints one JSON line: throughput, the dominant kernel's roofline (the
@@ -208,8 +209,8 @@ def main():
         tower_ms, launches, layers = r.time_tower_convs(0, B, args.conv_iters)
         conv_ms = tower_ms / launches
         layers_per_launch = layers // launches
-        # The tower as the pass runs it (a large batch as two half-batch
-        # chains on two streams): the effective time per layer of the batch.
+        # The tower as the pass runs it (two half-batch chains on two streams
+        # where the pass splits): the effective time per layer of the batch.
         pass_tower_ms, pass_layers = r.time_tower_layers(0, B, args.conv_iters)
         layer_ms = pass_tower_ms / pass_layers
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
@@ -263,6 +264,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": traffic,
+            # HBM bandwidth of one launch from the counters: traffic / launch time.
+            "traffic_gb_s": round(traffic / (conv_ms * 1e-3) / 1e9, 1) if traffic else None,
             "avg_launch_ms": round(conv_ms, 4),
             "per_layer_ms": round(layer_ms, 4),
             "per_layer_frac": round(w.trunk_conv_flops(B) / (layer_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
