@@ -28,6 +28,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -202,8 +203,10 @@ def main():
         ms_per_step = dt * 1e3 / args.steps
         value = B * args.steps / dt
 
-        # The same passes timed with HIP events on the pass's stream.
+        # The same passes timed with HIP events on the pass's stream, and the
+        # median of single passes, each timed on its own.
         ev_ms = r.time_passes(0, B, args.steps) / args.steps
+        ev_median_ms = statistics.median(r.time_passes(0, B, 1) for _ in range(args.steps))
         # The dominant kernel: the residual tower's 3x3 convolutions, timed as
         # the pass runs them (every block's two launches in order).
         tower_ms, launches, layers = r.time_tower_convs(0, B, args.conv_iters)
@@ -215,6 +218,7 @@ def main():
         layer_ms = pass_tower_ms / pass_layers
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
         rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
+        rt_median_ms = statistics.median(r.time_round_trips(0, B, 1) for _ in range(max(3, args.steps // 5)))
         # Both slots kept full through begin/done, each pass with its own
         # pinned copies (the reference bench's "2-slot" GPU rate).
         two_slot = None
@@ -254,7 +258,9 @@ def main():
         "pct_fp32_mfma_peak": round(100 * pass_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
         "pass_tflops": round(pass_tflops, 2),
         "event_ms_per_step": round(ev_ms, 4),
+        "event_median_ms_per_pass": round(ev_median_ms, 4),
         "round_trip_ms": round(rt_ms, 4),
+        "round_trip_median_ms": round(rt_median_ms, 4),
         "two_slot_positions_per_s": two_slot,
         "roofline": {
             "kernel": kernel_name,
