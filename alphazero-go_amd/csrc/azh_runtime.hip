@@ -778,6 +778,13 @@ struct azh_runner {
     //   two slots).
     bool splitPass(int B) const {
         if (B < 2) return false;
+        // A layer of under 0.5 GFLOP of matrix work (3 us at the fp32 MFMA
+        // peak) is bound by its launch, and a second chain's launches only
+        // add to it (5x5 4x32, 300 boards: 0.14 GFLOP per layer, 5.4 ->
+        // 10.9 us per layer in halves).
+        const double layerFlops = 2.0 * B * shape.A * 16.0 * azh::ceilDiv(shape.F, azh::kCoBlock) * 16.0 *
+                                  azh::ceilDiv(shape.F, azh::kChunk) * 9.0;
+        if (layerFlops < 0.5e9) return false;
         const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
         const long workgroups = azh::convWorkgroups(t, shape.F, B, shape.n);
         const long cus = azh::deviceCUs();

@@ -193,13 +193,14 @@ def test_shape_and_split_boundaries(hip, B):
             assert bitwise_equal(alone[0][0], whole[0][s]) and bitwise_equal(alone[1][0], whole[1][s]), s
 
 
-@pytest.mark.parametrize("B", [128, 129, 191, 192])
-def test_small_shape_split_boundaries(hip, B):
+@pytest.mark.parametrize("tag,B", [(2, 128), (2, 129), (2, 191), (2, 192), (1, 1085), (1, 1086)])
+def test_small_board_split_boundaries(hip, tag, B):
     """9x9 6x64 around the smaller shapes' split (two chains past two rounds
     of workgroups, from 129 boards) and the change to whole-board
-    workgroups at 192 boards (one chain again): rows on both sides of the
-    halves are the bits of their positions alone."""
-    w = O.WORKLOADS[2]
+    workgroups at 192 boards (one chain again); 5x5 4x32 around the least
+    layer work that splits (0.5 GFLOP, from 1086 boards): rows on both
+    sides of the halves are the bits of their positions alone."""
+    w = O.WORKLOADS[tag]
     net = O.random_network(w.cfg, 608)
     inp, _ = O.workload_inputs(w, B)
     with _runner(hip, net, B) as r:
