@@ -95,6 +95,7 @@ def load():
             "azh_evaluate_positions": ([vp, P(Positions), C.c_int, f32, f32, u8, f32], C.c_int),
             "azh_time_positions": ([vp, P(Positions), C.c_int, C.c_int, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
+            "azh_set_small_tower": ([vp, C.c_int], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_enqueue": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_synchronize": ([vp, C.c_int], C.c_int),
@@ -342,6 +343,9 @@ class Runner:
 
     def set_graphs(self, enabled):
         _check(self.lib.azh_set_graphs(self.h, int(enabled)))
+
+    def set_small_tower(self, enabled):
+        _check(self.lib.azh_set_small_tower(self.h, int(enabled)))
 
     # ---- slot staging (the hub's view)
     def input(self, slot):

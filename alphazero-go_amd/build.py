@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libazgo_hip.so")
-SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip"]
+SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip", "azh_small_tower.hip"]
 # The 3x3 convolution is one template instantiated per (board size,
 # workgroup shape): azh_conv_inst.hip is compiled once per pair, so the
 # fully unrolled kernels build in parallel.

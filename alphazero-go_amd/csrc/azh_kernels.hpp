@@ -37,6 +37,20 @@ size_t headPolicyWTFloats(int n);
 size_t headFc1WTFloats(int n, int V);
 // Compute units of the current device (cached; 256 if the query fails).
 int deviceCUs();
+
+// The whole residual tower of a 5x5 or 9x9 board of up to 64 channels in
+// one launch, one workgroup per board with its activations in LDS
+// (azh_small_tower.hip):
+// `layers` (even) convolutions on trunk [B][ceil(F/4)][n*n] quads in place,
+// layer l's packed weights at w0 + l * layerStride floats and its BN scale
+// and shift at scaleOff and shiftOff floats after them. The same bits as
+// the per-layer launches. smallTowerLdsBytes: the LDS a workgroup needs (0
+// for other boards); launches need at most kSmallTowerMaxLds.
+constexpr size_t kSmallTowerMaxLds = 64 * 1024;
+constexpr int kSmallTowerMaxChunks = 4;   // up to 64 channels: one channel block per wave
+size_t smallTowerLdsBytes(int n, int F);
+hipError_t launchSmallTower(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
+                            int layers, int B, int n, int F, hipStream_t stream);
 // Workgroups of one convolution launch of shape t over B boards of
 // boardSize x boardSize with cout output channels (the launcher's grid).
 long convWorkgroups(ConvTiling t, int cout, int B, int boardSize);

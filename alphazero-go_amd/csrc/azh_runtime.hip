@@ -685,6 +685,15 @@ struct azh_runner {
     DeviceWeights weights;
     std::vector<std::unique_ptr<Slot>> slots;
     bool graphs = true;
+    // The whole tower in one launch on small boards (azh::launchSmallTower):
+    // allowed (a test hook turns it off), and the tower convolutions' place
+    // in the weight arena (one fixed stride; `tower.ok` once checked).
+    bool smallTower = true;
+    struct TowerLayout {
+        bool ok = false;
+        const float* w0 = nullptr;
+        size_t stride = 0, scaleOff = 0, shiftOff = 0;
+    } tower;
 
     struct Pass {
         int slot;
@@ -741,7 +750,7 @@ struct azh_runner {
     // shape t (the shape decides only which workgroup computes an output,
     // never how, so a part's bits are the whole batch's).
     void launchPassPart(Slot& s, int b0, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun,
-                        bool heads) {
+                        bool heads, bool small) {
         const Shape& sh = shape;
         const size_t trunk = azh::quadFloats(1, sh.F, sh.A);   // floats per board
         float* x = s.dX + b0 * trunk;
@@ -749,12 +758,57 @@ struct azh_runner {
         check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
                                  weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
               "conv3x3 (stem)");
-        launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
+        if (small)
+            check(azh::launchSmallTower(x, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+                                        2 * std::max(blocksToRun, 0), Bp, sh.n, sh.F, stream),
+                  "small-board tower");
+        else
+            launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
         if (heads)
             check(azh::launchHeads(x, weights.heads, s.dAct + (size_t)b0 * 3 * sh.A, s.dLogits + (size_t)b0 * sh.A1,
                                    s.dValues + b0, s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr, Bp, sh.n, sh.F,
                                    sh.V, stream),
                   "heads");
+    }
+
+    // Checks that the tower's convolutions sit in the weight arena at one
+    // fixed stride (conv1 and conv2 of each block in turn, each with its BN
+    // scale and shift at fixed offsets after its packed weights), as the
+    // small-board tower kernel reads them.
+    void initTowerLayout() {
+        const std::vector<ConvW>& c1 = weights.conv1;
+        const std::vector<ConvW>& c2 = weights.conv2;
+        tower = TowerLayout{};
+        if (c1.empty() || c2.size() != c1.size()) return;
+        const float* w0 = c1[0].w;
+        if (c2[0].w <= w0 || c1[0].scale < w0 || c1[0].shift < w0) return;
+        const size_t stride = (size_t)(c2[0].w - w0), scaleOff = (size_t)(c1[0].scale - w0),
+                     shiftOff = (size_t)(c1[0].shift - w0);
+        for (size_t i = 0; i < c1.size(); ++i)
+            for (int h = 0; h < 2; ++h) {
+                const ConvW& c = h == 0 ? c1[i] : c2[i];
+                const float* w = w0 + (2 * i + h) * stride;
+                if (c.w != w || c.scale != w + scaleOff || c.shift != w + shiftOff) return;
+            }
+        tower = TowerLayout{true, w0, stride, scaleOff, shiftOff};
+    }
+
+    // Whether a pass of B runs its tower as one small-board launch: 5x5 up
+    // to 64 channels at any batch (5x5 4x32: 8 layers in 22.6 us against
+    // about 34 us as 8 launches at 8 boards, 23.2 against 45 at 256), 9x9 at
+    // 49 to 64 channels past 128 boards (9x9 6x64: 12 layers in 174 us
+    // against 218 at 256 boards; at 64 boards 172 against 108, since one
+    // board per workgroup leaves a layer at 14.5 us; at three chunks the 9x9
+    // instance keeps its fragment buffers in scratch, so not below 49).
+    bool useSmallTower(int B) const {
+        if (!smallTower || !tower.ok) return false;
+        const Shape& sh = shape;
+        if (azh::smallTowerLdsBytes(sh.n, sh.F) == 0 ||
+            azh::smallTowerLdsBytes(sh.n, sh.F) > azh::kSmallTowerMaxLds)
+            return false;
+        if (sh.n == 5) return sh.F <= 64;
+        if (sh.n == 9) return sh.F > 48 && sh.F <= 64 && B > 128;
+        return false;
     }
 
     // Whether a pass of B runs as two half-batch chains on two streams.
@@ -777,7 +831,7 @@ struct azh_runner {
     //   -18% with two slots; 19x19 20x256, 8 boards: +7% alone, -19% with
     //   two slots).
     bool splitPass(int B) const {
-        if (B < 2) return false;
+        if (B < 2 || useSmallTower(B)) return false;
         // A layer of under 0.5 GFLOP of matrix work (3 us at the fp32 MFMA
         // peak) is bound by its launch, and a second chain's launches only
         // add to it (5x5 4x32, 300 boards: 0.14 GFLOP per layer, 5.4 ->
@@ -826,14 +880,21 @@ struct azh_runner {
 
     // The pass's kernels, on `stream`, in halves when the pass splits.
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+        const bool small = useSmallTower(B);
         overHalves(s, B, stream, [&](int b0, int Bp, hipStream_t st) {
-            launchPassPart(s, b0, Bp, partTiling(B, Bp), st, blocksToRun, heads);
+            launchPassPart(s, b0, Bp, partTiling(B, Bp), st, blocksToRun, heads, small);
         });
     }
 
     // The tower as the pass runs it, on slot s's staged trunk (the effective
     // time per layer within a pass).
     void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
+        if (useSmallTower(B)) {
+            check(azh::launchSmallTower(s.dX, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+                                        2 * std::max(blocksToRun, 0), B, shape.n, shape.F, s.stream),
+                  "small-board tower");
+            return;
+        }
         const size_t trunk = azh::quadFloats(1, shape.F, shape.A);
         overHalves(s, B, s.stream, [&](int b0, int Bp, hipStream_t st) {
             launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, partTiling(B, Bp), st, blocksToRun);
@@ -846,7 +907,10 @@ struct azh_runner {
             launchPass(s, B, s.stream, shape.blocks, true);
             return;
         }
-        auto it = s.graphs.find(B);
+        // One graph per batch size and tower form (the small-board tower can
+        // be switched off by a test hook).
+        const int key = 2 * B + (useSmallTower(B) ? 1 : 0);
+        auto it = s.graphs.find(key);
         if (it == s.graphs.end()) {
             hipGraph_t g = nullptr;
             check(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -862,7 +926,7 @@ struct azh_runner {
             const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             check(e, "hipGraphInstantiate");
-            it = s.graphs.emplace(B, exec).first;
+            it = s.graphs.emplace(key, exec).first;
         }
         check(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
     }
@@ -1008,6 +1072,7 @@ void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, i
     checkFits((double)runnerBytes(*cfg, max_batch, slots), max_batch, 1);
     std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
     uploadWeights(*cfg, given, r->weights);
+    r->initTowerLayout();
     for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
     azh_runner* raw = r.get();
     r->completion = std::thread([raw] { raw->completionLoop(); });
@@ -1355,6 +1420,13 @@ int azh_set_graphs(azh_runner* r, int enabled) {
     return guarded([&] {
         if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
         r->graphs = enabled != 0;
+    });
+}
+
+int azh_set_small_tower(azh_runner* r, int enabled) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        r->smallTower = enabled != 0;
     });
 }
 

@@ -1,0 +1,203 @@
+// The residual tower of a small board in one launch: one workgroup per
+// board runs every block's two 3x3 convolutions with the board's activations
+// held in LDS (two haloed tiles in channel quads: the block input x and the
+// middle activation), so a pass of many short layers is one launch instead
+// of one per layer. Boards are independent, so no workgroup ever waits for
+// another.
+//
+// The arithmetic is the tower kernel's (azh_conv.hpp): the same packed A
+// fragments, the same B values (channel quads with zeros past the channel
+// count), the same order of v_mfma_f32_16x16x4_f32 per output (chunk, tap,
+// channel in chunk) and the same epilogue, so every output has the bits the
+// per-layer launches give it.
+#include "azh_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace azh {
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSmallThreads = 256;   // 4 waves
+
+template <int P>
+struct Parity {
+    static constexpr int value = P;
+};
+
+// trunk [B][ceil(F/4)][A] quads, in place; F <= 64, NQ = ceil(F/16) chunks
+// (and channel blocks). Layer l's packed weights start at w0 + l *
+// layerStride floats, its BN scale and shift at scaleOff and shiftOff floats
+// after them (the tower's convolutions sit in the weight arena at one fixed
+// stride). Wave w < NQ computes output channel block w over all of the
+// board's column groups; the A fragments (nine taps) of its next chunk, or of
+// the next layer's first, are fetched while the current chunk is multiplied.
+// The chunk loop is unrolled with the two fragment buffers assigned at
+// compile time (layers come in pairs, so the parity of a chunk's buffer is
+// known), which keeps each fetch a whole chunk ahead of its use.
+template <int N, int NQ>
+__global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restrict__ trunk,
+                                                                  const float* __restrict__ w0, size_t layerStride,
+                                                                  size_t scaleOff, size_t shiftOff, int layers,
+                                                                  int F) {
+    constexpr int A = N * N, H = N + 2, HA = H * H, NPG = (A + 15) / 16;
+    constexpr int G = 4 * NQ;   // channel quads held per tile (whole chunks; the padding stays zero)
+    extern __shared__ f4 tile[];
+    const int GQ = (F + 3) / 4;   // channel quads stored in the trunk
+    f4* tx = tile;
+    f4* tm = tile + G * HA;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = lane >> 4, n16 = lane & 15;
+    const int b = blockIdx.x;
+    f4* xq = reinterpret_cast<f4*>(trunk) + (size_t)b * GQ * A;
+
+    for (int i = tid; i < 2 * G * HA; i += kSmallThreads) tile[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();
+    for (int i = tid; i < GQ * A; i += kSmallThreads) {
+        const int g = i / A, p = i - g * A;
+        tx[g * HA + (p / N + 1) * H + (p % N + 1)] = xq[i];
+    }
+    __syncthreads();
+
+    if (wave >= NQ) {
+        for (int l = 0; l < layers; ++l) __syncthreads();
+    } else {
+        const int cb = wave;
+        // Each lane's top-left tap cell per column group; points past the
+        // board read a valid cell and are never stored.
+        int base[NPG];
+#pragma unroll
+        for (int j = 0; j < NPG; ++j) {
+            int p = j * 16 + n16;
+            p = p < A ? p : A - 1;
+            base[j] = (p / N) * H + (p % N);
+        }
+        f4 acc[NPG];
+        f4 fa[9], fb[9];
+        auto load = [&](f4(&f)[9], int l, int q) {
+            const f4* w = reinterpret_cast<const f4*>(w0 + (size_t)l * layerStride) + (size_t)((cb * NQ + q) * 9) * 64 +
+                          lane;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) f[t] = w[t * 64];
+        };
+        auto multiply = [&](const f4(&f)[9], const f4* src, int q) {
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const f4* s = src + (4 * q + k) * HA + (t / 3) * H + (t % 3);
+#pragma unroll
+                for (int j = 0; j < NPG; ++j) {
+                    const f4 bv = s[base[j]];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f[t][e], bv[e], acc[j], 0, 0, 0);
+                }
+            }
+        };
+        // Lane (n16, k) holds channels 16 cb + 4 k + e of point 16 j + n16;
+        // the second convolution of a block adds the block input it
+        // overwrites (the same lane reads and writes each element).
+        auto store = [&](int l, f4* dst, bool skip) {
+            const float* lw = w0 + (size_t)l * layerStride;
+            const int gch = cb * 4 + k;
+#pragma unroll
+            for (int j = 0; j < NPG; ++j) {
+                const int p = j * 16 + n16;
+                if (p < A) {
+                    f4* cell = dst + gch * HA + (p / N + 1) * H + (p % N + 1);
+                    const f4 sk = skip ? *cell : f4{0.0f, 0.0f, 0.0f, 0.0f};
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int c = gch * 4 + e;
+                        v[e] = c < F ? epilogue(acc[j][e], lw[scaleOff + c], lw[shiftOff + c], skip, sk[e], true)
+                                     : 0.0f;
+                    }
+                    *cell = v;
+                }
+            }
+        };
+        // One layer: chunk q's fragments are in buffer (P + q) & 1 (fa for
+        // 0), the next chunk's are fetched into the other before q is
+        // multiplied.
+        auto layer = [&](int l, auto parity) {
+            constexpr int P = decltype(parity)::value;
+            const bool second = l & 1;
+            const f4* src = second ? tm : tx;
+            f4* dst = second ? tx : tm;
+#pragma unroll
+            for (int j = 0; j < NPG; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            // Explicit branches, not a select between the two arrays: each
+            // branch names its buffers, so they stay in registers.
+            auto chunk = [&](f4(&cur)[9], f4(&next)[9], int q) {
+                if (q + 1 < NQ)
+                    load(next, l, q + 1);
+                else if (l + 1 < layers)
+                    load(next, l + 1, 0);
+                multiply(cur, src, q);
+            };
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                if (((P + q) & 1) == 0)
+                    chunk(fa, fb, q);
+                else
+                    chunk(fb, fa, q);
+            }
+            store(l, dst, second);
+            __syncthreads();   // the layer is complete
+        };
+        if (layers > 0) load(fa, 0, 0);
+        for (int l = 0; l < layers; l += 2) {
+            layer(l, Parity<0>{});
+            layer(l + 1, Parity<NQ & 1>{});
+        }
+    }
+
+    for (int i = tid; i < GQ * A; i += kSmallThreads) {
+        const int g = i / A, p = i - g * A;
+        xq[i] = tx[g * HA + (p / N + 1) * H + (p % N + 1)];
+    }
+}
+
+template <int N>
+constexpr size_t smallTileBytes(int F) {
+    return 2 * (size_t)(4 * ((F + 15) / 16)) * (N + 2) * (N + 2) * sizeof(f4);
+}
+
+} // namespace
+
+size_t smallTowerLdsBytes(int n, int F) {
+    if (n == 5) return smallTileBytes<5>(F);
+    if (n == 9) return smallTileBytes<9>(F);
+    return 0;
+}
+
+namespace {
+
+template <int N, int NQ = 1>
+hipError_t launchSmallN(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
+                        int layers, int B, int F, size_t lds, hipStream_t stream) {
+    if constexpr (NQ <= kSmallTowerMaxChunks) {
+        if ((F + 15) / 16 != NQ)
+            return launchSmallN<N, NQ + 1>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, w0,
+                           layerStride, scaleOff, shiftOff, layers, F);
+        return hipGetLastError();
+    } else {
+        return hipErrorInvalidValue;
+    }
+}
+
+} // namespace
+
+hipError_t launchSmallTower(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
+                            int layers, int B, int n, int F, hipStream_t stream) {
+    const size_t lds = smallTowerLdsBytes(n, F);
+    if (B < 1 || F < 1 || F > 16 * kSmallTowerMaxChunks || layers < 0 || (layers & 1) || lds == 0 ||
+        lds > kSmallTowerMaxLds)
+        return hipErrorInvalidValue;
+    if (n == 5) return launchSmallN<5>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    return launchSmallN<9>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+}
+
+} // namespace azh

@@ -210,6 +210,36 @@ def test_small_board_split_boundaries(hip, tag, B):
             assert bitwise_equal(alone[0][0], whole[0][s]) and bitwise_equal(alone[1][0], whole[1][s]), s
 
 
+@pytest.mark.parametrize("cfg,B", [
+    (O.make_cfg(5, 4, 32), 8),
+    (O.make_cfg(5, 4, 32), 300),
+    (O.make_cfg(5, 2, 30, value_hidden=16), 3),
+    (O.make_cfg(5, 2, 16, ownership=1), 5),
+    (O.make_cfg(5, 3, 64), 17),
+    (O.make_cfg(9, 6, 64), 160),
+    (O.make_cfg(9, 2, 56), 129),
+])
+def test_small_tower_equals_per_layer_launches(hip, cfg, B):
+    """A small board's tower in one launch (one workgroup per board, the
+    activations in LDS) gives the bits of the per-layer launches, graph and
+    eager, including ragged channel counts and the ownership head."""
+    net = O.random_network(cfg, 609)
+    w = O.Workload(0, "small", cfg, B, 0.3, 0.3)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B) as r:
+        one = r.infer(inp)
+        r.set_small_tower(False)
+        per_layer = r.infer(inp)
+        r.set_graphs(False)
+        eager = r.infer(inp)
+        r.set_small_tower(True)
+        one_eager = r.infer(inp)
+    for got in (per_layer, eager, one_eager):
+        assert len(got) == len(one)
+        for a, b in zip(got, one):
+            assert bitwise_equal(a, b)
+
+
 def test_repeatable_and_graph_equals_eager(hip):
     w = O.WORKLOADS[2]
     net = O.random_network(w.cfg, 604)
