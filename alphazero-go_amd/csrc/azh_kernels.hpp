@@ -46,11 +46,22 @@ int deviceCUs();
 // and shift at scaleOff and shiftOff floats after them. The same bits as
 // the per-layer launches. smallTowerLdsBytes: the LDS a workgroup needs (0
 // for other boards); launches need at most kSmallTowerMaxLds.
+// With a stem, the launch first runs the stem convolution from the
+// network's input planes [B][planes][n*n] (its packed weights, BN scale and
+// shift) into the trunk, as conv3x3Stem does; without one (nullptr or in ==
+// nullptr) it reads the trunk.
 constexpr size_t kSmallTowerMaxLds = 64 * 1024;
 constexpr int kSmallTowerMaxChunks = 4;   // up to 64 channels: one channel block per wave
-size_t smallTowerLdsBytes(int n, int F);
-hipError_t launchSmallTower(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
-                            int layers, int B, int n, int F, hipStream_t stream);
+struct SmallStem {
+    const float* in = nullptr;
+    const float* w = nullptr;
+    const float* scale = nullptr;
+    const float* shift = nullptr;
+    int planes = 0;
+};
+size_t smallTowerLdsBytes(int n, int F, int planes);
+hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const float* w0, size_t layerStride,
+                            size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F, hipStream_t stream);
 // Workgroups of one convolution launch of shape t over B boards of
 // boardSize x boardSize with cout output channels (the launcher's grid).
 long convWorkgroups(ConvTiling t, int cout, int B, int boardSize);

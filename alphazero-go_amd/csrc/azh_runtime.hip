@@ -755,15 +755,19 @@ struct azh_runner {
         const size_t trunk = azh::quadFloats(1, sh.F, sh.A);   // floats per board
         float* x = s.dX + b0 * trunk;
         float* mid = s.dMid + b0 * trunk;
-        check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
-                                 weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
-              "conv3x3 (stem)");
-        if (small)
-            check(azh::launchSmallTower(x, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+        if (small) {
+            // The stem and the tower in one launch.
+            const azh::SmallStem stem{s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
+                                      weights.stem.shift, sh.P};
+            check(azh::launchSmallTower(x, &stem, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
                                         2 * std::max(blocksToRun, 0), Bp, sh.n, sh.F, stream),
-                  "small-board tower");
-        else
+                  "small-board stem and tower");
+        } else {
+            check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
+                                     weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
+                  "conv3x3 (stem)");
             launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
+        }
         if (heads)
             check(azh::launchHeads(x, weights.heads, s.dAct + (size_t)b0 * 3 * sh.A, s.dLogits + (size_t)b0 * sh.A1,
                                    s.dValues + b0, s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr, Bp, sh.n, sh.F,
@@ -798,14 +802,13 @@ struct azh_runner {
     // about 34 us as 8 launches at 8 boards, 23.2 against 45 at 256), 9x9 at
     // 49 to 64 channels past 128 boards (9x9 6x64: 12 layers in 174 us
     // against 218 at 256 boards; at 64 boards 172 against 108, since one
-    // board per workgroup leaves a layer at 14.5 us; at three chunks the 9x9
-    // instance keeps its fragment buffers in scratch, so not below 49).
+    // board per workgroup leaves a layer at 14.5 us; not measured below 49
+    // channels).
     bool useSmallTower(int B) const {
         if (!smallTower || !tower.ok) return false;
         const Shape& sh = shape;
-        if (azh::smallTowerLdsBytes(sh.n, sh.F) == 0 ||
-            azh::smallTowerLdsBytes(sh.n, sh.F) > azh::kSmallTowerMaxLds)
-            return false;
+        const size_t lds = azh::smallTowerLdsBytes(sh.n, sh.F, sh.P);
+        if (lds == 0 || lds > azh::kSmallTowerMaxLds) return false;
         if (sh.n == 5) return sh.F <= 64;
         if (sh.n == 9) return sh.F > 48 && sh.F <= 64 && B > 128;
         return false;
@@ -890,7 +893,7 @@ struct azh_runner {
     // time per layer within a pass).
     void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
         if (useSmallTower(B)) {
-            check(azh::launchSmallTower(s.dX, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+            check(azh::launchSmallTower(s.dX, nullptr, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
                                         2 * std::max(blocksToRun, 0), B, shape.n, shape.F, s.stream),
                   "small-board tower");
             return;

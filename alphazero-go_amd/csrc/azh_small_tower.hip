@@ -36,9 +36,11 @@ struct Parity {
 // the next layer's first, are fetched while the current chunk is multiplied.
 // The chunk loop is unrolled with the two fragment buffers assigned at
 // compile time (layers come in pairs, so the parity of a chunk's buffer is
-// known), which keeps each fetch a whole chunk ahead of its use.
+// known), which keeps each fetch a whole chunk ahead of its use, and the
+// helpers are forced inline (left to the inliner, the 9x9 instances kept
+// their arrays in scratch memory).
 template <int N, int NQ>
-__global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restrict__ trunk,
+__global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restrict__ trunk, SmallStem stem,
                                                                   const float* __restrict__ w0, size_t layerStride,
                                                                   size_t scaleOff, size_t shiftOff, int layers,
                                                                   int F) {
@@ -46,21 +48,40 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     constexpr int G = 4 * NQ;   // channel quads held per tile (whole chunks; the padding stays zero)
     extern __shared__ f4 tile[];
     const int GQ = (F + 3) / 4;   // channel quads stored in the trunk
+    // With the stem, the second tile first holds the input planes in
+    // channel quads (whole 16-channel chunks, zero past the plane count).
+    const int GS = stem.in ? 4 * ((stem.planes + 15) / 16) : 0;
+    const int GM = G > GS ? G : GS;
     f4* tx = tile;
     f4* tm = tile + G * HA;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = lane >> 4, n16 = lane & 15;
     const int b = blockIdx.x;
     f4* xq = reinterpret_cast<f4*>(trunk) + (size_t)b * GQ * A;
 
-    for (int i = tid; i < 2 * G * HA; i += kSmallThreads) tile[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = tid; i < (G + GM) * HA; i += kSmallThreads) tile[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();
-    for (int i = tid; i < GQ * A; i += kSmallThreads) {
-        const int g = i / A, p = i - g * A;
-        tx[g * HA + (p / N + 1) * H + (p % N + 1)] = xq[i];
+    if (stem.in) {
+        // The input planes [P][A] of this board, a channel at a time (the
+        // stem kernel's staging): channels past P read as zeros.
+        const float* in = stem.in + (size_t)b * stem.planes * A;
+        for (int i = tid; i < GS * A; i += kSmallThreads) {
+            const int g = i / A, p = i - g * A;
+            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (4 * g + c < stem.planes) v[c] = in[(size_t)(4 * g + c) * A + p];
+            tm[g * HA + (p / N + 1) * H + (p % N + 1)] = v;
+        }
+    } else {
+        for (int i = tid; i < GQ * A; i += kSmallThreads) {
+            const int g = i / A, p = i - g * A;
+            tx[g * HA + (p / N + 1) * H + (p % N + 1)] = xq[i];
+        }
     }
     __syncthreads();
 
     if (wave >= NQ) {
+        if (stem.in) __syncthreads();
         for (int l = 0; l < layers; ++l) __syncthreads();
     } else {
         const int cb = wave;
@@ -75,13 +96,13 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
         }
         f4 acc[NPG];
         f4 fa[9], fb[9];
-        auto load = [&](f4(&f)[9], int l, int q) {
+        auto load = [&](f4(&f)[9], int l, int q) __attribute__((always_inline)) {
             const f4* w = reinterpret_cast<const f4*>(w0 + (size_t)l * layerStride) + (size_t)((cb * NQ + q) * 9) * 64 +
                           lane;
 #pragma unroll
             for (int t = 0; t < 9; ++t) f[t] = w[t * 64];
         };
-        auto multiply = [&](const f4(&f)[9], const f4* src, int q) {
+        auto multiply = [&](const f4(&f)[9], const f4* src, int q) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < 9; ++t) {
                 const f4* s = src + (4 * q + k) * HA + (t / 3) * H + (t % 3);
@@ -97,8 +118,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
         // Lane (n16, k) holds channels 16 cb + 4 k + e of point 16 j + n16;
         // the second convolution of a block adds the block input it
         // overwrites (the same lane reads and writes each element).
-        auto store = [&](int l, f4* dst, bool skip) {
-            const float* lw = w0 + (size_t)l * layerStride;
+        auto store = [&](const float* sc, const float* sh, f4* dst, bool skip) __attribute__((always_inline)) {
             const int gch = cb * 4 + k;
 #pragma unroll
             for (int j = 0; j < NPG; ++j) {
@@ -110,8 +130,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int c = gch * 4 + e;
-                        v[e] = c < F ? epilogue(acc[j][e], lw[scaleOff + c], lw[shiftOff + c], skip, sk[e], true)
-                                     : 0.0f;
+                        v[e] = c < F ? epilogue(acc[j][e], sc[c], sh[c], skip, sk[e], true) : 0.0f;
                     }
                     *cell = v;
                 }
@@ -120,7 +139,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
         // One layer: chunk q's fragments are in buffer (P + q) & 1 (fa for
         // 0), the next chunk's are fetched into the other before q is
         // multiplied.
-        auto layer = [&](int l, auto parity) {
+        auto layer = [&](int l, auto parity) __attribute__((always_inline)) {
             constexpr int P = decltype(parity)::value;
             const bool second = l & 1;
             const f4* src = second ? tm : tx;
@@ -129,7 +148,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
             for (int j = 0; j < NPG; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             // Explicit branches, not a select between the two arrays: each
             // branch names its buffers, so they stay in registers.
-            auto chunk = [&](f4(&cur)[9], f4(&next)[9], int q) {
+            auto chunk = [&](f4(&cur)[9], f4(&next)[9], int q) __attribute__((always_inline)) {
                 if (q + 1 < NQ)
                     load(next, l, q + 1);
                 else if (l + 1 < layers)
@@ -143,10 +162,27 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
                 else
                     chunk(fb, fa, q);
             }
-            store(l, dst, second);
+            const float* lw = w0 + (size_t)l * layerStride;
+            store(lw + scaleOff, lw + shiftOff, dst, second);
             __syncthreads();   // the layer is complete
         };
         if (layers > 0) load(fa, 0, 0);
+        if (stem.in) {
+            // The stem: input planes (in tm) -> x, BN and ReLU, no skip; its
+            // fragments are fetched a chunk at a time (one layer only).
+#pragma unroll
+            for (int j = 0; j < NPG; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int nqs = GS / 4;
+            for (int q = 0; q < nqs; ++q) {
+                f4 fs[9];
+                const f4* w = reinterpret_cast<const f4*>(stem.w) + (size_t)((cb * nqs + q) * 9) * 64 + lane;
+#pragma unroll
+                for (int t = 0; t < 9; ++t) fs[t] = w[t * 64];
+                multiply(fs, tm, q);
+            }
+            store(stem.scale, stem.shift, tx, false);
+            __syncthreads();   // x is complete and the input tile is free
+        }
         for (int l = 0; l < layers; l += 2) {
             layer(l, Parity<0>{});
             layer(l + 1, Parity<NQ & 1>{});
@@ -159,28 +195,24 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     }
 }
 
-template <int N>
-constexpr size_t smallTileBytes(int F) {
-    return 2 * (size_t)(4 * ((F + 15) / 16)) * (N + 2) * (N + 2) * sizeof(f4);
-}
-
 } // namespace
 
-size_t smallTowerLdsBytes(int n, int F) {
-    if (n == 5) return smallTileBytes<5>(F);
-    if (n == 9) return smallTileBytes<9>(F);
-    return 0;
+size_t smallTowerLdsBytes(int n, int F, int planes) {
+    if (n != 5 && n != 9) return 0;
+    const size_t g = 4 * (size_t)((F + 15) / 16), gs = planes > 0 ? 4 * (size_t)((planes + 15) / 16) : 0;
+    return (g + (g > gs ? g : gs)) * (size_t)(n + 2) * (n + 2) * sizeof(f4);
 }
 
 namespace {
 
 template <int N, int NQ = 1>
-hipError_t launchSmallN(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
-                        int layers, int B, int F, size_t lds, hipStream_t stream) {
+hipError_t launchSmallN(float* trunk, const SmallStem& stem, const float* w0, size_t layerStride, size_t scaleOff,
+                        size_t shiftOff, int layers, int B, int F, size_t lds, hipStream_t stream) {
     if constexpr (NQ <= kSmallTowerMaxChunks) {
         if ((F + 15) / 16 != NQ)
-            return launchSmallN<N, NQ + 1>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
-        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, w0,
+            return launchSmallN<N, NQ + 1>(trunk, stem, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds,
+                                           stream);
+        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, stem, w0,
                            layerStride, scaleOff, shiftOff, layers, F);
         return hipGetLastError();
     } else {
@@ -190,14 +222,16 @@ hipError_t launchSmallN(float* trunk, const float* w0, size_t layerStride, size_
 
 } // namespace
 
-hipError_t launchSmallTower(float* trunk, const float* w0, size_t layerStride, size_t scaleOff, size_t shiftOff,
-                            int layers, int B, int n, int F, hipStream_t stream) {
-    const size_t lds = smallTowerLdsBytes(n, F);
+hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const float* w0, size_t layerStride,
+                            size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F, hipStream_t stream) {
+    const SmallStem st = stem ? *stem : SmallStem{};
+    if (st.in && (st.planes < 1 || !st.w || !st.scale || !st.shift)) return hipErrorInvalidValue;
+    const size_t lds = smallTowerLdsBytes(n, F, st.in ? st.planes : 0);
     if (B < 1 || F < 1 || F > 16 * kSmallTowerMaxChunks || layers < 0 || (layers & 1) || lds == 0 ||
         lds > kSmallTowerMaxLds)
         return hipErrorInvalidValue;
-    if (n == 5) return launchSmallN<5>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
-    return launchSmallN<9>(trunk, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    if (n == 5) return launchSmallN<5>(trunk, st, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    return launchSmallN<9>(trunk, st, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
 }
 
 } // namespace azh
