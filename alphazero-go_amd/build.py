@@ -23,7 +23,7 @@ SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip", "azh_small
 CONV_INST = "azh_conv_inst.hip"
 CONV_HEADERS = ["azh_conv.hpp", "azh_conv_iface.hpp"]
 BOARD_SIZES = (5, 9, 13, 19)   # conv3x3Supported
-HEADERS = CONV_HEADERS + ["azh_kernels.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
+HEADERS = CONV_HEADERS + ["azh_kernels.hpp", "azh_heads.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

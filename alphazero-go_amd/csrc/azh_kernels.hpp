@@ -59,9 +59,20 @@ struct SmallStem {
     const float* shift = nullptr;
     int planes = 0;
 };
-size_t smallTowerLdsBytes(int n, int F, int planes);
-hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const float* w0, size_t layerStride,
-                            size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F, hipStream_t stream);
+// With heads (logits set), the launch ends with the heads on the board's
+// trunk, as launchHeads computes them: logits [B][n*n+1], values [B], and
+// with own set the ownership [B][n*n]; the trunk is written back either way.
+struct SmallHeads {
+    HeadWeights w{};
+    float* logits = nullptr;
+    float* values = nullptr;
+    float* own = nullptr;
+    int V = 0;
+};
+size_t smallTowerLdsBytes(int n, int F, int planes, bool heads, int V);
+hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const SmallHeads* heads, const float* w0,
+                            size_t layerStride, size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F,
+                            hipStream_t stream);
 // Workgroups of one convolution launch of shape t over B boards of
 // boardSize x boardSize with cout output channels (the launcher's grid).
 long convWorkgroups(ConvTiling t, int cout, int B, int boardSize);

@@ -685,7 +685,7 @@ struct azh_runner {
     DeviceWeights weights;
     std::vector<std::unique_ptr<Slot>> slots;
     bool graphs = true;
-    // The whole tower in one launch on small boards (azh::launchSmallTower):
+    // The whole pass in one launch on small boards (azh::launchSmallTower):
     // allowed (a test hook turns it off), and the tower convolutions' place
     // in the weight arena (one fixed stride; `tower.ok` once checked).
     bool smallTower = true;
@@ -756,18 +756,26 @@ struct azh_runner {
         float* x = s.dX + b0 * trunk;
         float* mid = s.dMid + b0 * trunk;
         if (small) {
-            // The stem and the tower in one launch.
+            // The stem, the tower and the heads in one launch.
             const azh::SmallStem stem{s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
                                       weights.stem.shift, sh.P};
-            check(azh::launchSmallTower(x, &stem, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+            azh::SmallHeads hd;
+            if (heads) {
+                hd.w = weights.heads;
+                hd.logits = s.dLogits + (size_t)b0 * sh.A1;
+                hd.values = s.dValues + b0;
+                hd.own = s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr;
+                hd.V = sh.V;
+            }
+            check(azh::launchSmallTower(x, &stem, &hd, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
                                         2 * std::max(blocksToRun, 0), Bp, sh.n, sh.F, stream),
-                  "small-board stem and tower");
-        } else {
-            check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
-                                     weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
-                  "conv3x3 (stem)");
-            launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
+                  "small-board pass");
+            return;
         }
+        check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
+                                 weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
+              "conv3x3 (stem)");
+        launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
         if (heads)
             check(azh::launchHeads(x, weights.heads, s.dAct + (size_t)b0 * 3 * sh.A, s.dLogits + (size_t)b0 * sh.A1,
                                    s.dValues + b0, s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr, Bp, sh.n, sh.F,
@@ -797,17 +805,17 @@ struct azh_runner {
         tower = TowerLayout{true, w0, stride, scaleOff, shiftOff};
     }
 
-    // Whether a pass of B runs its tower as one small-board launch: 5x5 up
-    // to 64 channels at any batch (5x5 4x32: 8 layers in 22.6 us against
-    // about 34 us as 8 launches at 8 boards, 23.2 against 45 at 256), 9x9 at
-    // 49 to 64 channels past 128 boards (9x9 6x64: 12 layers in 174 us
-    // against 218 at 256 boards; at 64 boards 172 against 108, since one
-    // board per workgroup leaves a layer at 14.5 us; not measured below 49
-    // channels).
+    // Whether a pass of B runs as one small-board launch (stem, tower,
+    // heads): 5x5 up to 64 channels at any batch (5x5 4x32 per pass: 37.4
+    // against 46.5 us as per-layer launches at 8 boards, 39.9 against 60.1
+    // at 256), 9x9 at 49 to 64 channels past 128 boards (9x9 6x64: 213.1
+    // against 235.6 us at 256 boards; at 64 boards the tower alone took 172
+    // against 108 us, since one board per workgroup leaves a layer at 14.5
+    // us; not measured below 49 channels).
     bool useSmallTower(int B) const {
         if (!smallTower || !tower.ok) return false;
         const Shape& sh = shape;
-        const size_t lds = azh::smallTowerLdsBytes(sh.n, sh.F, sh.P);
+        const size_t lds = azh::smallTowerLdsBytes(sh.n, sh.F, sh.P, true, sh.V);
         if (lds == 0 || lds > azh::kSmallTowerMaxLds) return false;
         if (sh.n == 5) return sh.F <= 64;
         if (sh.n == 9) return sh.F > 48 && sh.F <= 64 && B > 128;
@@ -893,8 +901,9 @@ struct azh_runner {
     // time per layer within a pass).
     void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
         if (useSmallTower(B)) {
-            check(azh::launchSmallTower(s.dX, nullptr, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
-                                        2 * std::max(blocksToRun, 0), B, shape.n, shape.F, s.stream),
+            check(azh::launchSmallTower(s.dX, nullptr, nullptr, tower.w0, tower.stride, tower.scaleOff,
+                                        tower.shiftOff, 2 * std::max(blocksToRun, 0), B, shape.n, shape.F,
+                                        s.stream),
                   "small-board tower");
             return;
         }

@@ -1,18 +1,22 @@
-// The residual tower of a small board in one launch: one workgroup per
-// board runs every block's two 3x3 convolutions with the board's activations
-// held in LDS (two haloed tiles in channel quads: the block input x and the
-// middle activation), so a pass of many short layers is one launch instead
-// of one per layer. Boards are independent, so no workgroup ever waits for
-// another.
+// A small board's pass in one launch: one workgroup per board runs the
+// stem, every block's two 3x3 convolutions and the heads with the board's
+// activations held in LDS (two haloed tiles in channel quads: the block
+// input x and the middle activation), so a pass of many short layers is one
+// launch instead of one per layer. Boards are independent, so no workgroup
+// ever waits for another.
 //
-// The arithmetic is the tower kernel's (azh_conv.hpp): the same packed A
-// fragments, the same B values (channel quads with zeros past the channel
-// count), the same order of v_mfma_f32_16x16x4_f32 per output (chunk, tap,
-// channel in chunk) and the same epilogue, so every output has the bits the
-// per-layer launches give it.
+// The arithmetic is the per-layer kernels': for the convolutions the tower
+// kernel's (azh_conv.hpp) packed A fragments, B values (channel quads with
+// zeros past the channel count), order of v_mfma_f32_16x16x4_f32 per output
+// (chunk, tap, channel in chunk) and epilogue; for the heads the order of
+// headConvKernel's sums and headFcKernel's MFMA blocks. Every output has
+// the bits the per-layer launches give it.
 #include "azh_kernels.hpp"
+#include "azh_heads.hpp"
 
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 namespace azh {
 
@@ -41,6 +45,7 @@ struct Parity {
 // their arrays in scratch memory).
 template <int N, int NQ>
 __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restrict__ trunk, SmallStem stem,
+                                                                  SmallHeads heads,
                                                                   const float* __restrict__ w0, size_t layerStride,
                                                                   size_t scaleOff, size_t shiftOff, int layers,
                                                                   int F) {
@@ -193,27 +198,90 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
         const int g = i / A, p = i - g * A;
         xq[i] = tx[g * HA + (p / N + 1) * H + (p % N + 1)];
     }
+    if (!heads.logits) return;
+
+    // The heads on the trunk in tx, as headConvKernel and headFcKernel
+    // compute them (the same sums in the same order): the 1x1 convolutions
+    // per point, then the policy and value Linears as 16-row MFMA blocks
+    // whose row 0 is this board (the other 15 rows zero). The second tile is
+    // free: the staged rows [16][RS], the value plane [A], the hidden [V].
+    constexpr int A1 = A + 1, KP = headPad16(2 * A), KV = headPad16(A), NP = headPad16(A1), RS = KP + 4;
+    const HeadWeights& hw = heads.w;
+    float* xs = reinterpret_cast<float*>(tm);
+    float* valRow = xs + 16 * RS;
+    float* hid = valRow + A;
+    const int m = lane & 15, kk = lane >> 4;
+    for (int i = tid; i < 16 * RS; i += kSmallThreads) xs[i] = 0.0f;
+    __syncthreads();
+    for (int p = tid; p < A; p += kSmallThreads) {
+        const f4* xp = tx + (p / N + 1) * H + (p % N + 1);
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (int c = 0; c < F; ++c) {
+            const float x = xp[(c / 4) * HA][c % 4];
+            a0 = fmaf(hw.convW[c], x, a0);
+            a1 = fmaf(hw.convW[F + c], x, a1);
+            a2 = fmaf(hw.convW[2 * F + c], x, a2);
+            if (heads.own) a3 = fmaf(hw.convW[3 * F + c], x, a3);
+        }
+        xs[p] = epilogue(a0, hw.scale[0], hw.shift[0], false, 0.0f, true);       // feature c*A + p
+        xs[A + p] = epilogue(a1, hw.scale[1], hw.shift[1], false, 0.0f, true);
+        valRow[p] = epilogue(a2, hw.scale[2], hw.shift[2], false, 0.0f, true);
+        if (heads.own)
+            heads.own[(size_t)b * A + p] = tanhf(epilogue(a3, hw.scale[3], hw.shift[3], false, 0.0f, false));
+    }
+    __syncthreads();
+    const HeadVec4* xs4 = reinterpret_cast<const HeadVec4*>(xs);
+    for (int n0 = wave * 16; n0 < NP; n0 += 64) {
+        const HeadVec4 acc = fcBlock<KP, RS>(xs4, m, kk, n0, NP, hw.policyWT);
+        const int a = n0 + m;
+        if (kk == 0 && a < A1) heads.logits[(size_t)b * A1 + a] = __fadd_rn(acc[0], hw.policyB[a]);
+    }
+    __syncthreads();
+    for (int i = tid; i < KV; i += kSmallThreads) xs[i] = i < A ? valRow[i] : 0.0f;
+    __syncthreads();
+    const int V = heads.V, VP = headPad16(V);
+    for (int n0 = wave * 16; n0 < VP; n0 += 64) {
+        const HeadVec4 acc = fcBlock<KV, RS>(xs4, m, kk, n0, VP, hw.fc1WT);
+        const int v = n0 + m;
+        if (kk == 0 && v < V) {
+            const float h = __fadd_rn(acc[0], hw.fc1B[v]);
+            hid[v] = h > 0.0f ? h : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.0f;
+        for (int u = 0; u < V; ++u) s = fmaf(hid[u], hw.fc2W[u], s);
+        heads.values[b] = tanhf(__fadd_rn(s, hw.fc2B[0]));
+    }
 }
 
 } // namespace
 
-size_t smallTowerLdsBytes(int n, int F, int planes) {
+size_t smallTowerLdsBytes(int n, int F, int planes, bool heads, int V) {
     if (n != 5 && n != 9) return 0;
+    const size_t cell = (size_t)(n + 2) * (n + 2) * sizeof(f4);
     const size_t g = 4 * (size_t)((F + 15) / 16), gs = planes > 0 ? 4 * (size_t)((planes + 15) / 16) : 0;
-    return (g + (g > gs ? g : gs)) * (size_t)(n + 2) * (n + 2) * sizeof(f4);
+    size_t second = (g > gs ? g : gs) * cell;
+    if (heads) {   // the heads' rows, value plane and hidden layer in the second tile
+        const size_t A = (size_t)n * n, rows = 16 * (size_t)(headPad16(2 * n * n) + 4) + A + (size_t)V;
+        second = std::max(second, rows * sizeof(float));
+    }
+    return g * cell + second;
 }
 
 namespace {
 
 template <int N, int NQ = 1>
-hipError_t launchSmallN(float* trunk, const SmallStem& stem, const float* w0, size_t layerStride, size_t scaleOff,
-                        size_t shiftOff, int layers, int B, int F, size_t lds, hipStream_t stream) {
+hipError_t launchSmallN(float* trunk, const SmallStem& stem, const SmallHeads& heads, const float* w0,
+                        size_t layerStride, size_t scaleOff, size_t shiftOff, int layers, int B, int F, size_t lds,
+                        hipStream_t stream) {
     if constexpr (NQ <= kSmallTowerMaxChunks) {
         if ((F + 15) / 16 != NQ)
-            return launchSmallN<N, NQ + 1>(trunk, stem, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds,
-                                           stream);
-        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, stem, w0,
-                           layerStride, scaleOff, shiftOff, layers, F);
+            return launchSmallN<N, NQ + 1>(trunk, stem, heads, w0, layerStride, scaleOff, shiftOff, layers, B, F,
+                                           lds, stream);
+        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, stem, heads,
+                           w0, layerStride, scaleOff, shiftOff, layers, F);
         return hipGetLastError();
     } else {
         return hipErrorInvalidValue;
@@ -222,16 +290,20 @@ hipError_t launchSmallN(float* trunk, const SmallStem& stem, const float* w0, si
 
 } // namespace
 
-hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const float* w0, size_t layerStride,
-                            size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F, hipStream_t stream) {
+hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const SmallHeads* heads, const float* w0,
+                            size_t layerStride, size_t scaleOff, size_t shiftOff, int layers, int B, int n, int F,
+                            hipStream_t stream) {
     const SmallStem st = stem ? *stem : SmallStem{};
+    const SmallHeads hd = heads ? *heads : SmallHeads{};
     if (st.in && (st.planes < 1 || !st.w || !st.scale || !st.shift)) return hipErrorInvalidValue;
-    const size_t lds = smallTowerLdsBytes(n, F, st.in ? st.planes : 0);
+    if (hd.logits && (!hd.values || hd.V < 1 || hd.V > 256)) return hipErrorInvalidValue;
+    const size_t lds = smallTowerLdsBytes(n, F, st.in ? st.planes : 0, hd.logits != nullptr, hd.V);
     if (B < 1 || F < 1 || F > 16 * kSmallTowerMaxChunks || layers < 0 || (layers & 1) || lds == 0 ||
         lds > kSmallTowerMaxLds)
         return hipErrorInvalidValue;
-    if (n == 5) return launchSmallN<5>(trunk, st, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
-    return launchSmallN<9>(trunk, st, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    if (n == 5)
+        return launchSmallN<5>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    return launchSmallN<9>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
 }
 
 } // namespace azh

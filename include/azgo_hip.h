@@ -235,10 +235,10 @@ int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters
 int azh_set_graphs(azh_runner* r, int enabled);
 
 /* Whether a small board's pass (5x5 up to 64 channels; 9x9 at 49 to 64
- * channels past 128 boards) runs its residual tower as one launch, one
- * workgroup per board with the activations in LDS (default 1), or as one
- * launch per convolution. Both give the same bits. No counterpart in the
- * reference (its CUDA runner launches per layer); a test hook. */
+ * channels past 128 boards) runs as one launch (stem, residual tower and
+ * heads), one workgroup per board with the activations in LDS (default 1),
+ * or as one launch per layer. Both give the same bits. No counterpart in
+ * the reference (its CUDA runner launches per layer); a test hook. */
 int azh_set_small_tower(azh_runner* r, int enabled);
 
 /* ---------------------------------------------------------------- device-resident passes (measurement) */
