@@ -806,8 +806,8 @@ struct azh_runner {
     }
 
     // Whether a pass of B runs as one small-board launch (stem, tower,
-    // heads): 5x5 up to 64 channels at any batch (5x5 4x32 per pass: 37.4
-    // against 46.5 us as per-layer launches at 8 boards, 39.9 against 60.1
+    // heads): 5x5 up to 64 channels at any batch (5x5 4x32 per pass: 26.8
+    // against 46.2 us as per-layer launches at 8 boards, 29.6 against 60.0
     // at 256), 9x9 at 49 to 64 channels past 128 boards (9x9 6x64: 213.1
     // against 235.6 us at 256 boards; at 64 boards the tower alone took 172
     // against 108 us, since one board per workgroup leaves a layer at 14.5

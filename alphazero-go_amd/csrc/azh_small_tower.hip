@@ -35,9 +35,9 @@ struct Parity {
 // (and channel blocks). Layer l's packed weights start at w0 + l *
 // layerStride floats, its BN scale and shift at scaleOff and shiftOff floats
 // after them (the tower's convolutions sit in the weight arena at one fixed
-// stride). Wave w < NQ computes output channel block w over all of the
-// board's column groups; the A fragments (nine taps) of its next chunk, or of
-// the next layer's first, are fetched while the current chunk is multiplied.
+// stride). Each channel block goes to 4 / NQ waves, which share its column
+// groups; the A fragments (nine taps) of a wave's next chunk, or of the next
+// layer's first, are fetched while the current chunk is multiplied.
 // The chunk loop is unrolled with the two fragment buffers assigned at
 // compile time (layers come in pairs, so the parity of a chunk's buffer is
 // known), which keeps each fetch a whole chunk ahead of its use, and the
@@ -85,21 +85,27 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     }
     __syncthreads();
 
-    if (wave >= NQ) {
+    // With fewer channel blocks than waves, a block's column groups are
+    // split over 4 / NQ waves (PGW each), so every wave has work where the
+    // board allows (the split decides only which wave computes an output).
+    constexpr int WPB = 4 / NQ;                    // waves per channel block
+    constexpr int PGW = (NPG + WPB - 1) / WPB;     // column groups per wave
+    const int cb = wave / WPB, pg0 = (wave % WPB) * PGW;
+    if (cb >= NQ || pg0 >= NPG) {
         if (stem.in) __syncthreads();
         for (int l = 0; l < layers; ++l) __syncthreads();
     } else {
-        const int cb = wave;
         // Each lane's top-left tap cell per column group; points past the
-        // board read a valid cell and are never stored.
-        int base[NPG];
+        // board (and column groups past the board's) read a valid cell and
+        // are never stored.
+        int base[PGW];
 #pragma unroll
-        for (int j = 0; j < NPG; ++j) {
-            int p = j * 16 + n16;
+        for (int j = 0; j < PGW; ++j) {
+            int p = (pg0 + j) * 16 + n16;
             p = p < A ? p : A - 1;
             base[j] = (p / N) * H + (p % N);
         }
-        f4 acc[NPG];
+        f4 acc[PGW];
         f4 fa[9], fb[9];
         auto load = [&](f4(&f)[9], int l, int q) __attribute__((always_inline)) {
             const f4* w = reinterpret_cast<const f4*>(w0 + (size_t)l * layerStride) + (size_t)((cb * NQ + q) * 9) * 64 +
@@ -112,7 +118,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
             for (int t = 0; t < 9; ++t) {
                 const f4* s = src + (4 * q + k) * HA + (t / 3) * H + (t % 3);
 #pragma unroll
-                for (int j = 0; j < NPG; ++j) {
+                for (int j = 0; j < PGW; ++j) {
                     const f4 bv = s[base[j]];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -120,14 +126,15 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
                 }
             }
         };
-        // Lane (n16, k) holds channels 16 cb + 4 k + e of point 16 j + n16;
-        // the second convolution of a block adds the block input it
-        // overwrites (the same lane reads and writes each element).
+        // Lane (n16, k) holds channels 16 cb + 4 k + e of point
+        // 16 (pg0 + j) + n16; the second convolution of a block adds the
+        // block input it overwrites (the same lane reads and writes each
+        // element).
         auto store = [&](const float* sc, const float* sh, f4* dst, bool skip) __attribute__((always_inline)) {
             const int gch = cb * 4 + k;
 #pragma unroll
-            for (int j = 0; j < NPG; ++j) {
-                const int p = j * 16 + n16;
+            for (int j = 0; j < PGW; ++j) {
+                const int p = (pg0 + j) * 16 + n16;
                 if (p < A) {
                     f4* cell = dst + gch * HA + (p / N + 1) * H + (p % N + 1);
                     const f4 sk = skip ? *cell : f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -150,7 +157,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
             const f4* src = second ? tm : tx;
             f4* dst = second ? tx : tm;
 #pragma unroll
-            for (int j = 0; j < NPG; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < PGW; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             // Explicit branches, not a select between the two arrays: each
             // branch names its buffers, so they stay in registers.
             auto chunk = [&](f4(&cur)[9], f4(&next)[9], int q) __attribute__((always_inline)) {
@@ -176,7 +183,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
             // The stem: input planes (in tm) -> x, BN and ReLU, no skip; its
             // fragments are fetched a chunk at a time (one layer only).
 #pragma unroll
-            for (int j = 0; j < NPG; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < PGW; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             const int nqs = GS / 4;
             for (int q = 0; q < nqs; ++q) {
                 f4 fs[9];
