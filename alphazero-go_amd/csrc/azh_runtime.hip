@@ -1022,7 +1022,19 @@ struct azh_runner {
               "hipMemcpyAsync(values)");
     }
 
-    static hipError_t waitFor(hipEvent_t e) { return hipEventSynchronize(e); }
+    // A pass's completion: polled for up to kCompletionPollUs (a small
+    // network's pass ends within it, and the driver's wake-up from a
+    // blocking wait costs tens of microseconds), then slept on.
+    static constexpr int kCompletionPollUs = 50;
+    static hipError_t waitFor(hipEvent_t e) {
+        const auto until = std::chrono::steady_clock::now() + std::chrono::microseconds(kCompletionPollUs);
+        for (;;) {
+            const hipError_t q = hipEventQuery(e);
+            if (q != hipErrorNotReady) return q;
+            if (std::chrono::steady_clock::now() >= until) break;
+        }
+        return hipEventSynchronize(e);
+    }
 
     void completionLoop() {
         for (;;) {
