@@ -24,7 +24,12 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSmallThreads = 256;   // 4 waves
+// 4 waves per board. (8 on 9x9, a channel block's 6 column groups split
+// 3 and 3, measured 3% faster up to 256 boards and 9% slower at 512, where
+// two 8-wave workgroups no longer fit a CU: a 9x9 board's layer is bound by
+// its CU's matrix rate, about 10 us, either way.)
+template <int N>
+constexpr int smallThreads() { return 256; }
 
 template <int P>
 struct Parity {
@@ -35,8 +40,8 @@ struct Parity {
 // (and channel blocks). Layer l's packed weights start at w0 + l *
 // layerStride floats, its BN scale and shift at scaleOff and shiftOff floats
 // after them (the tower's convolutions sit in the weight arena at one fixed
-// stride). Each channel block goes to 4 / NQ waves, which share its column
-// groups; the A fragments (nine taps) of a wave's next chunk, or of the next
+// stride). Each channel block goes to waves / NQ waves, which share its
+// column groups; the A fragments (nine taps) of a wave's next chunk, or of the next
 // layer's first, are fetched while the current chunk is multiplied.
 // The chunk loop is unrolled with the two fragment buffers assigned at
 // compile time (layers come in pairs, so the parity of a chunk's buffer is
@@ -44,12 +49,13 @@ struct Parity {
 // helpers are forced inline (left to the inliner, the 9x9 instances kept
 // their arrays in scratch memory).
 template <int N, int NQ>
-__global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restrict__ trunk, SmallStem stem,
+__global__ __launch_bounds__(smallThreads<N>()) void smallTowerKernel(float* __restrict__ trunk, SmallStem stem,
                                                                   SmallHeads heads,
                                                                   const float* __restrict__ w0, size_t layerStride,
                                                                   size_t scaleOff, size_t shiftOff, int layers,
                                                                   int F) {
     constexpr int A = N * N, H = N + 2, HA = H * H, NPG = (A + 15) / 16;
+    constexpr int THREADS = smallThreads<N>(), WAVES = THREADS / 64;
     constexpr int G = 4 * NQ;   // channel quads held per tile (whole chunks; the padding stays zero)
     extern __shared__ f4 tile[];
     const int GQ = (F + 3) / 4;   // channel quads stored in the trunk
@@ -63,13 +69,13 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     const int b = blockIdx.x;
     f4* xq = reinterpret_cast<f4*>(trunk) + (size_t)b * GQ * A;
 
-    for (int i = tid; i < (G + GM) * HA; i += kSmallThreads) tile[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = tid; i < (G + GM) * HA; i += THREADS) tile[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();
     if (stem.in) {
         // The input planes [P][A] of this board, a channel at a time (the
         // stem kernel's staging): channels past P read as zeros.
         const float* in = stem.in + (size_t)b * stem.planes * A;
-        for (int i = tid; i < GS * A; i += kSmallThreads) {
+        for (int i = tid; i < GS * A; i += THREADS) {
             const int g = i / A, p = i - g * A;
             f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
             tm[g * HA + (p / N + 1) * H + (p % N + 1)] = v;
         }
     } else {
-        for (int i = tid; i < GQ * A; i += kSmallThreads) {
+        for (int i = tid; i < GQ * A; i += THREADS) {
             const int g = i / A, p = i - g * A;
             tx[g * HA + (p / N + 1) * H + (p % N + 1)] = xq[i];
         }
@@ -86,9 +92,10 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     __syncthreads();
 
     // With fewer channel blocks than waves, a block's column groups are
-    // split over 4 / NQ waves (PGW each), so every wave has work where the
-    // board allows (the split decides only which wave computes an output).
-    constexpr int WPB = 4 / NQ;                    // waves per channel block
+    // split over WAVES / NQ waves (PGW each), so every wave has work where
+    // the board allows (the split decides only which wave computes an
+    // output).
+    constexpr int WPB = WAVES / NQ;                // waves per channel block
     constexpr int PGW = (NPG + WPB - 1) / WPB;     // column groups per wave
     const int cb = wave / WPB, pg0 = (wave % WPB) * PGW;
     if (cb >= NQ || pg0 >= NPG) {
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
         }
     }
 
-    for (int i = tid; i < GQ * A; i += kSmallThreads) {
+    for (int i = tid; i < GQ * A; i += THREADS) {
         const int g = i / A, p = i - g * A;
         xq[i] = tx[g * HA + (p / N + 1) * H + (p % N + 1)];
     }
@@ -218,9 +225,9 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     float* valRow = xs + 16 * RS;
     float* hid = valRow + A;
     const int m = lane & 15, kk = lane >> 4;
-    for (int i = tid; i < 16 * RS; i += kSmallThreads) xs[i] = 0.0f;
+    for (int i = tid; i < 16 * RS; i += THREADS) xs[i] = 0.0f;
     __syncthreads();
-    for (int p = tid; p < A; p += kSmallThreads) {
+    for (int p = tid; p < A; p += THREADS) {
         const f4* xp = tx + (p / N + 1) * H + (p % N + 1);
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
         for (int c = 0; c < F; ++c) {
@@ -238,16 +245,16 @@ __global__ __launch_bounds__(kSmallThreads) void smallTowerKernel(float* __restr
     }
     __syncthreads();
     const HeadVec4* xs4 = reinterpret_cast<const HeadVec4*>(xs);
-    for (int n0 = wave * 16; n0 < NP; n0 += 64) {
+    for (int n0 = wave * 16; n0 < NP; n0 += 16 * WAVES) {
         const HeadVec4 acc = fcBlock<KP, RS>(xs4, m, kk, n0, NP, hw.policyWT);
         const int a = n0 + m;
         if (kk == 0 && a < A1) heads.logits[(size_t)b * A1 + a] = __fadd_rn(acc[0], hw.policyB[a]);
     }
     __syncthreads();
-    for (int i = tid; i < KV; i += kSmallThreads) xs[i] = i < A ? valRow[i] : 0.0f;
+    for (int i = tid; i < KV; i += THREADS) xs[i] = i < A ? valRow[i] : 0.0f;
     __syncthreads();
     const int V = heads.V, VP = headPad16(V);
-    for (int n0 = wave * 16; n0 < VP; n0 += 64) {
+    for (int n0 = wave * 16; n0 < VP; n0 += 16 * WAVES) {
         const HeadVec4 acc = fcBlock<KV, RS>(xs4, m, kk, n0, VP, hw.fc1WT);
         const int v = n0 + m;
         if (kk == 0 && v < V) {
@@ -287,7 +294,7 @@ hipError_t launchSmallN(float* trunk, const SmallStem& stem, const SmallHeads& h
         if ((F + 15) / 16 != NQ)
             return launchSmallN<N, NQ + 1>(trunk, stem, heads, w0, layerStride, scaleOff, shiftOff, layers, B, F,
                                            lds, stream);
-        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(kSmallThreads), lds, stream, trunk, stem, heads,
+        hipLaunchKernelGGL((smallTowerKernel<N, NQ>), dim3(B), dim3(smallThreads<N>()), lds, stream, trunk, stem, heads,
                            w0, layerStride, scaleOff, shiftOff, layers, F);
         return hipGetLastError();
     } else {
