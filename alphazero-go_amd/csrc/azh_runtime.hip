@@ -808,17 +808,19 @@ struct azh_runner {
     // Whether a pass of B runs as one small-board launch (stem, tower,
     // heads): 5x5 up to 64 channels at any batch (5x5 4x32 per pass: 26.8
     // against 46.2 us as per-layer launches at 8 boards, 29.6 against 60.0
-    // at 256), 9x9 at 49 to 64 channels past 128 boards (9x9 6x64: 213.1
-    // against 235.6 us at 256 boards; at 64 boards the tower alone took 172
-    // against 108 us, since one board per workgroup leaves a layer at 14.5
-    // us; not measured below 49 channels).
+    // at 256); 9x9 up to 32 channels at any batch (6x16: 41.7 against 65.1
+    // us at 8 boards; 6x32: 73.7 against 75.8 at 8, 75.5 against 124.2 at
+    // 256) and up to 64 past 128 boards (6x48: 168.8 against 210.8 us at
+    // 256, 167.5 against 153.9 at 128; 6x64: 214.7 against 235.4 at 256,
+    // 212.5 against 186.3 at 128: a board's pass in one workgroup runs at
+    // its CU's matrix rate, about 200 us at 64 channels whatever the batch).
     bool useSmallTower(int B) const {
         if (!smallTower || !tower.ok) return false;
         const Shape& sh = shape;
         const size_t lds = azh::smallTowerLdsBytes(sh.n, sh.F, sh.P, true, sh.V);
         if (lds == 0 || lds > azh::kSmallTowerMaxLds) return false;
         if (sh.n == 5) return sh.F <= 64;
-        if (sh.n == 9) return sh.F > 48 && sh.F <= 64 && B > 128;
+        if (sh.n == 9) return sh.F <= 32 || (sh.F <= 64 && B > 128);
         return false;
     }
 

@@ -218,6 +218,8 @@ def test_small_board_split_boundaries(hip, tag, B):
     (O.make_cfg(5, 3, 64), 17),
     (O.make_cfg(9, 6, 64), 160),
     (O.make_cfg(9, 2, 56), 129),
+    (O.make_cfg(9, 3, 32), 8),
+    (O.make_cfg(9, 2, 20, value_hidden=16, ownership=1), 6),
 ])
 def test_small_tower_equals_per_layer_launches(hip, cfg, B):
     """A small board's tower in one launch (one workgroup per board, the
