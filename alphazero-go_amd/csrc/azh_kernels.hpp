@@ -38,8 +38,8 @@ size_t headFc1WTFloats(int n, int V);
 // Compute units of the current device (cached; 256 if the query fails).
 int deviceCUs();
 
-// The whole residual tower of a 5x5 or 9x9 board of up to 64 channels in
-// one launch, one workgroup per board with its activations in LDS
+// The whole residual tower of a 5x5, 9x9 or 13x13 board of up to 64
+// channels (as LDS allows) in one launch, one workgroup per board with its activations in LDS
 // (azh_small_tower.hip):
 // `layers` (even) convolutions on trunk [B][ceil(F/4)][n*n] quads in place,
 // layer l's packed weights at w0 + l * layerStride floats and its BN scale

@@ -813,7 +813,11 @@ struct azh_runner {
     // 256) and up to 64 past 128 boards (6x48: 168.8 against 210.8 us at
     // 256, 167.5 against 153.9 at 128; 6x64: 214.7 against 235.4 at 256,
     // 212.5 against 186.3 at 128: a board's pass in one workgroup runs at
-    // its CU's matrix rate, about 200 us at 64 channels whatever the batch).
+    // its CU's matrix rate, about 200 us at 64 channels whatever the batch);
+    // 13x13 up to 16 channels at any batch (6x16: 59.1 against 70.9 us at
+    // 8 boards, 60.3 against 122.2 at 256) and up to 32 past 100 boards
+    // (6x32: 132.6 against 150.2 at 128, 131.7 against 105.4 at 64; two
+    // 13x13 tiles of 32 channels fill 57.6 of the 64 KB).
     bool useSmallTower(int B) const {
         if (!smallTower || !tower.ok) return false;
         const Shape& sh = shape;
@@ -821,6 +825,7 @@ struct azh_runner {
         if (lds == 0 || lds > azh::kSmallTowerMaxLds) return false;
         if (sh.n == 5) return sh.F <= 64;
         if (sh.n == 9) return sh.F <= 32 || (sh.F <= 64 && B > 128);
+        if (sh.n == 13) return sh.F <= 16 || (sh.F <= 32 && B > 100);
         return false;
     }
 

@@ -273,7 +273,7 @@ __global__ __launch_bounds__(smallThreads<N>()) void smallTowerKernel(float* __r
 } // namespace
 
 size_t smallTowerLdsBytes(int n, int F, int planes, bool heads, int V) {
-    if (n != 5 && n != 9) return 0;
+    if (n != 5 && n != 9 && n != 13) return 0;
     const size_t cell = (size_t)(n + 2) * (n + 2) * sizeof(f4);
     const size_t g = 4 * (size_t)((F + 15) / 16), gs = planes > 0 ? 4 * (size_t)((planes + 15) / 16) : 0;
     size_t second = (g > gs ? g : gs) * cell;
@@ -317,7 +317,9 @@ hipError_t launchSmallTower(float* trunk, const SmallStem* stem, const SmallHead
         return hipErrorInvalidValue;
     if (n == 5)
         return launchSmallN<5>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
-    return launchSmallN<9>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    if (n == 9)
+        return launchSmallN<9>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
+    return launchSmallN<13>(trunk, st, hd, w0, layerStride, scaleOff, shiftOff, layers, B, F, lds, stream);
 }
 
 } // namespace azh

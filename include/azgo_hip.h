@@ -235,7 +235,8 @@ int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters
 int azh_set_graphs(azh_runner* r, int enabled);
 
 /* Whether a small board's pass (5x5 up to 64 channels; 9x9 up to 32
- * channels, and up to 64 past 128 boards) runs as one launch (stem, residual tower and
+ * channels, and up to 64 past 128 boards; 13x13 up to 16 channels, and up
+ * to 32 past 100 boards) runs as one launch (stem, residual tower and
  * heads), one workgroup per board with the activations in LDS (default 1),
  * or as one launch per layer. Both give the same bits. No counterpart in
  * the reference (its CUDA runner launches per layer); a test hook. */

@@ -220,6 +220,8 @@ def test_small_board_split_boundaries(hip, tag, B):
     (O.make_cfg(9, 2, 56), 129),
     (O.make_cfg(9, 3, 32), 8),
     (O.make_cfg(9, 2, 20, value_hidden=16, ownership=1), 6),
+    (O.make_cfg(13, 2, 16), 5),
+    (O.make_cfg(13, 2, 32, value_hidden=256), 101),
 ])
 def test_small_tower_equals_per_layer_launches(hip, cfg, B):
     """A small board's tower in one launch (one workgroup per board, the
