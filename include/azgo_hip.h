@@ -231,15 +231,18 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
 int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters, float* ms);
 
 /* Whether passes replay a captured hipGraph per batch size (default 1), or
- * launch their kernels one by one. */
+ * launch their kernels one by one. Read when a pass is enqueued: set it
+ * while no other thread is beginning a pass. */
 int azh_set_graphs(azh_runner* r, int enabled);
 
 /* Whether a small board's pass (5x5 up to 64 channels; 9x9 up to 32
  * channels, and up to 64 past 128 boards; 13x13 up to 16 channels, and up
  * to 32 past 100 boards) runs as one launch (stem, residual tower and
  * heads), one workgroup per board with the activations in LDS (default 1),
- * or as one launch per layer. Both give the same bits. No counterpart in
- * the reference (its CUDA runner launches per layer); a test hook. */
+ * or as one launch per layer. Both give the same bits. Read when a pass is
+ * enqueued: set it while no other thread is beginning a pass. No
+ * counterpart in the reference (its CUDA runner launches per layer); a test
+ * hook. */
 int azh_set_small_tower(azh_runner* r, int enabled);
 
 /* ---------------------------------------------------------------- device-resident passes (measurement) */
