@@ -49,6 +49,11 @@ class Positions(C.Structure):
                 ("seen", C.POINTER(C.c_uint64)), ("seen_offsets", C.POINTER(C.c_int64))]
 
 
+class HubGroup(C.Structure):
+    """azh_hub_group: GpuHubs (include/azgo/gpu_memory.hpp)."""
+    _fields_ = [("hubs", C.c_int), ("slots_per_hub", C.c_int), ("max_batch", C.c_int)]
+
+
 DONE_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_char_p)
 
 
@@ -74,7 +79,7 @@ def load():
             "azh_last_error": ([], C.c_char_p),
             "azh_memory_need": ([P(NetCfg), C.c_int, C.c_int, P(C.c_size_t)], C.c_int),
             "azh_check_memory": ([P(NetCfg), C.c_int, C.c_int, C.c_int], C.c_int),
-            "azh_check_memory_bytes": ([C.c_double, C.c_int, C.c_int], C.c_int),
+            "azh_check_memory_groups": ([P(NetCfg), P(HubGroup), C.c_int], C.c_int),
             "azh_create": ([P(NetCfg), P(Tensor), C.c_int, C.c_int, C.c_int, P(vp)], C.c_int),
             "azh_tensor_count": ([P(NetCfg), P(C.c_int)], C.c_int),
             "azh_tensor_info": ([P(NetCfg), C.c_int, C.c_char_p, C.c_size_t, P(C.c_size_t)], C.c_int),
@@ -166,6 +171,12 @@ def memory_need(cfg, max_batch, slots):
 
 def check_memory(cfg, max_batch, hubs, slots_per_hub=2):
     _check(load().azh_check_memory(C.byref(cfg), max_batch, hubs, slots_per_hub))
+
+
+def check_memory_groups(cfg, groups):
+    """groups: (hubs, slots_per_hub, max_batch) triples, summed as one check."""
+    arr = (HubGroup * max(1, len(groups)))(*[HubGroup(*g) for g in groups])
+    _check(load().azh_check_memory_groups(C.byref(cfg), arr, len(groups)))
 
 
 def _u8(a):

@@ -19,11 +19,11 @@
 #include <condition_variable>
 #include <cstdio>
 #include <cstring>
-#include <deque>
 #include <fstream>
 #include <map>
 #include <memory>
 #include <mutex>
+#include <semaphore.h>
 #include <stdexcept>
 #include <string>
 #include <thread>
@@ -66,15 +66,27 @@ int guarded(Fn&& fn) {
     }
 }
 
-// Test hooks (cuda_probe's, src/cuda/cuda_runner.cu:39-45).
-std::atomic<uint64_t> gHubChaosSeed{0};
-std::atomic<int> gFailCountdown{0};
-std::atomic<size_t> gMemoryLimit{0};
-std::atomic<long long> gPassesCompleted{0};
-std::atomic<int> gCopyOutDelayUs{0};
+// The process-wide test hooks behind the azh_set_* / azh_fail_* entry points
+// (their meaning is cuda_probe's, include/azgo/cuda.hpp:138-155). Every
+// pass any runner reports gets the next report index; an injected failure
+// names the index it hits, so it fires once, on exactly one pass, whichever
+// runner's reporter gets there.
+struct TestHooks {
+    std::atomic<uint64_t> hubChaosSeed{0};
+    std::atomic<long long> reports{0};         // passes reported so far
+    std::atomic<long long> failingReport{-1};  // the report index to fail; -1: none
+    std::atomic<size_t> memoryLimit{0};        // 0: the device's own free memory
+    std::atomic<int> copyOutDelayUs{0};
 
-// Free memory a check leaves for everything else (src/cuda/cuda_runner.cu:50).
-constexpr size_t kMemoryMargin = size_t(512) << 20;
+    // Called once per reported pass: its report index, and whether the
+    // injected failure lands on it.
+    bool takeReport() {
+        long long index = reports.fetch_add(1);
+        return failingReport.compare_exchange_strong(index, -1);
+    }
+};
+TestHooks gHooks;
+
 constexpr int kMaxSlots = 2;   // kInferenceSlots (include/azgo/inference_hub.hpp:56)
 // The workgroup shapes a probe may force (include/azgo_hip.h lists them).
 const azh::ConvTiling* const kTilings = azh::kConvTilings;
@@ -577,8 +589,17 @@ struct Slot {
     float *dIn = nullptr, *dX = nullptr, *dMid = nullptr, *dAct = nullptr, *dLogits = nullptr, *dValues = nullptr;
     float* dOwn = nullptr;   // [B][A] after tanh, only with the ownership head
     float *hIn = nullptr, *hLogits = nullptr, *hValues = nullptr;
-    std::map<int, hipGraphExec_t> graphs;
-    bool busy = false;
+    // Captured passes by key (batch size and tower form), with the last
+    // time each was replayed (a count of replays on this slot), so the
+    // least recently replayed one goes when the cache is full.
+    struct CachedGraph {
+        hipGraphExec_t exec;
+        unsigned long long lastUse;
+    };
+    std::map<int, CachedGraph> graphs;
+    unsigned long long replays = 0;
+    // Set while a pass or a synchronous call holds the slot.
+    std::atomic<bool> claimed{false};
     // The positions path (azh_evaluate_positions), allocated on first use:
     // stones [maxBatch][H][A], plies, side to move, symmetry, superko list
     // offsets, legal [maxBatch][A+1], mapped logits and priors, and the
@@ -620,7 +641,7 @@ struct Slot {
     ~Slot() {
         if (stream) (void)hipStreamSynchronize(stream);
         if (aux) (void)hipStreamSynchronize(aux);
-        for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
+        for (auto& g : graphs) (void)hipGraphExecDestroy(g.second.exec);
         if (event) (void)hipEventDestroy(event);
         if (fork) (void)hipEventDestroy(fork);
         if (join) (void)hipEventDestroy(join);
@@ -633,23 +654,60 @@ struct Slot {
     }
 };
 
-double freeForCheck() {
-    const size_t limit = gMemoryLimit.load();
-    if (limit > 0) return (double)limit;
-    size_t freeBytes = 0, total = 0;
-    check(hipMemGetInfo(&freeBytes, &total), "hipMemGetInfo");
-    return freeBytes > kMemoryMargin ? (double)(freeBytes - kMemoryMargin) : 0.0;
+// Holds a slot for a synchronous call's scope, so that neither a pass begun
+// meanwhile nor another call can use its buffers and streams.
+class SlotClaim {
+public:
+    Slot& slot;
+    SlotClaim(Slot& s, int index) : slot(s) {
+        bool idle = false;
+        if (!s.claimed.compare_exchange_strong(idle, true))
+            throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(index) + " has a pass in flight");
+    }
+    ~SlotClaim() { slot.claimed.store(false, std::memory_order_release); }
+    SlotClaim(const SlotClaim&) = delete;
+    SlotClaim& operator=(const SlotClaim&) = delete;
+};
+
+// ---------------------------------------------------------------- memory admission
+
+// Device bytes that runners may still take: the device's free memory less a
+// 512 MB reserve kept for the HIP runtime and the rest of the process (the
+// reserve the reference's CUDA runner keeps, src/cuda/cuda_runner.cu:50), or
+// the test hook's stand-in when one is set.
+double spendableDeviceBytes() {
+    if (const size_t limit = gHooks.memoryLimit.load()) return (double)limit;
+    size_t freeBytes = 0, totalBytes = 0;
+    check(hipMemGetInfo(&freeBytes, &totalBytes), "hipMemGetInfo");
+    constexpr double kReserve = 512.0 * 1024 * 1024;
+    return std::max(0.0, (double)freeBytes - kReserve);
 }
 
-// checkFits (src/cuda/cuda_runner.cu:206-223), with its message.
-void checkFits(double need, int maxBatch, int hubs) {
-    const double have = freeForCheck();
-    if (need <= have) return;
-    throw Error(AZH_ERR_MEMORY, "hip: inference needs " + std::to_string((long long)(need / 1e6)) +
-                                    " MB of GPU memory at inference_batch " + std::to_string(maxBatch) +
-                                    (hubs > 1 ? " (" + std::to_string(hubs) + " hubs)" : std::string()) +
-                                    ", more than the " + std::to_string((long long)(have / 1e6)) +
-                                    " MB the GPU has free; lower inference_batch");
+// Every runner a process holds on the GPU at once, as groups of identical
+// runners (GpuHubs, include/azgo/gpu_memory.hpp), admitted or refused as one
+// sum. The refusal's wording is the reference's, which its callers and
+// users read (src/cuda/cuda_runner.cu:206-223): whole MB, the hub count when
+// above one, the largest batch, and "lower inference_batch" last.
+void admitRunners(const azh_netcfg& cfg, const azh_hub_group* groups, int count) {
+    if (count < 1 || !groups) throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: no hubs");
+    double need = 0.0;
+    int hubs = 0, widest = 0;
+    for (const azh_hub_group* g = groups; g != groups + count; ++g) {
+        if (g->hubs < 1 || g->slots_per_hub < 1 || g->max_batch < 1)
+            throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: bad arguments");
+        need += (double)g->hubs * (double)runnerBytes(cfg, g->max_batch, g->slots_per_hub);
+        hubs += g->hubs;
+        widest = std::max(widest, g->max_batch);
+    }
+    requireContext();
+    const double room = spendableDeviceBytes();
+    if (need <= room) return;
+    const auto wholeMB = [](double bytes) { return std::to_string((long long)(bytes / 1e6)); };
+    std::string refusal = "hip: inference needs " + wholeMB(need) + " MB of GPU memory at inference_batch " +
+                          std::to_string(widest);
+    if (hubs > 1) refusal += " (" + std::to_string(hubs) + " hubs)";
+    refusal += ", more than the " + wholeMB(room) + " MB the GPU has free; lower inference_batch";
+    throw Error(AZH_ERR_MEMORY, refusal);
 }
 
 template <class Body>
@@ -674,6 +732,101 @@ float timeOnStream(hipStream_t stream, int iters, Body body) {
     return ms;
 }
 
+// ---------------------------------------------------------------- the reporter
+
+// Reports a runner's passes: calls each pass's done exactly once, in the
+// order the passes were begun, from a thread of its own, once the event the
+// pass recorded behind its copy-out has fired (BatchRunner::begin's contract,
+// include/azgo/inference_hub.hpp:47-50).
+//
+// A slot holds at most one pass, so no more than kMaxSlots notices, plus the
+// closing one, are ever waiting: they sit in a fixed ring, and a counting
+// semaphore hands each to the thread. Closing posts a last notice that the
+// thread reaches only after every earlier one, so every pass begun before
+// it is reported before the thread ends and the slots may go.
+class Reporter {
+public:
+    struct Notice {
+        int slot = -1;                        // -1: the closing notice
+        hipEvent_t event = nullptr;           // recorded after the pass's copy-out
+        std::atomic<bool>* claim = nullptr;   // the slot's claim, released before done
+        azh_done_fn done = nullptr;
+        void* user = nullptr;
+        std::string error;                    // from enqueueing the pass, if that failed
+    };
+
+    Reporter() {
+        if (sem_init(&posted_, 0, 0) != 0) throw Error(AZH_ERR_HIP, "hip: cannot create the reporter's semaphore");
+    }
+    ~Reporter() {
+        close();
+        sem_destroy(&posted_);
+    }
+    Reporter(const Reporter&) = delete;
+    Reporter& operator=(const Reporter&) = delete;
+
+    void start() { thread_ = std::thread([this] { run(); }); }
+
+    // Hands a begun pass (or the closing notice) to the thread.
+    void post(Notice notice) {
+        {
+            std::lock_guard<std::mutex> lock(writing_);
+            if (written_ - taken_.load(std::memory_order_acquire) >= kRing)
+                throw Error(AZH_ERR_STATE, "hip: more passes waiting to be reported than the runner has slots");
+            ring_[written_ % kRing] = std::move(notice);
+            ++written_;
+        }
+        sem_post(&posted_);
+    }
+
+    // Reports every pass posted so far, then ends the thread.
+    void close() {
+        if (!thread_.joinable()) return;
+        post(Notice{});
+        thread_.join();
+    }
+
+private:
+    static constexpr size_t kRing = kMaxSlots + 1;
+
+    // A pass's end: polled for up to kPollUs (a small network's pass ends
+    // within it, and the driver's wake-up from a blocking wait costs tens of
+    // microseconds), then slept on (the slots' events are blocking-sync).
+    static constexpr int kPollUs = 50;
+    static hipError_t waitFor(hipEvent_t e) {
+        const auto until = std::chrono::steady_clock::now() + std::chrono::microseconds(kPollUs);
+        for (;;) {
+            const hipError_t q = hipEventQuery(e);
+            if (q != hipErrorNotReady) return q;
+            if (std::chrono::steady_clock::now() >= until) break;
+        }
+        return hipEventSynchronize(e);
+    }
+
+    void run() {
+        for (size_t next = 0;; ++next) {
+            while (sem_wait(&posted_) != 0) {   // only a signal interrupts it
+            }
+            Notice n = std::move(ring_[next % kRing]);
+            taken_.store(next + 1, std::memory_order_release);
+            if (n.slot < 0) return;
+            std::string error = std::move(n.error);
+            const hipError_t e = waitFor(n.event);
+            if (error.empty() && e != hipSuccess) error = std::string("hip: ") + hipGetErrorString(e);
+            if (gHooks.takeReport() && error.empty()) error = "hip: injected failure (a test hook)";
+            n.claim->store(false, std::memory_order_release);   // done may begin the slot again
+            n.done(n.user, n.slot, error.empty() ? nullptr : error.c_str());
+        }
+    }
+
+    Notice ring_[kRing];
+    std::mutex writing_;      // begin may come from more than one thread
+    size_t written_ = 0;      // under writing_
+    std::atomic<size_t> taken_{0};
+    sem_t posted_;
+    std::thread thread_;
+};
+
 } // namespace
 
 // ---------------------------------------------------------------- the runner
@@ -695,29 +848,14 @@ struct azh_runner {
         size_t stride = 0, scaleOff = 0, shiftOff = 0;
     } tower;
 
-    struct Pass {
-        int slot;
-        azh_done_fn done;
-        void* user;
-        std::string error;
-    };
-    std::mutex mutex;
-    std::condition_variable wake;
-    std::deque<Pass> queue;
-    bool stop = false;
-    std::thread completion;
+    Reporter reporter;
 
     azh_runner(const azh_netcfg& c, int mb) : cfg(c), shape(c), maxBatch(mb) {}
 
+    // The reporter goes first: closing it reports every pass begun, whose
+    // slots (events, pinned outputs) must still be there meanwhile.
     ~azh_runner() {
-        if (completion.joinable()) {
-            {
-                std::lock_guard<std::mutex> lock(mutex);
-                stop = true;
-            }
-            wake.notify_all();
-            completion.join();   // after every pass in flight has been reported
-        }
+        reporter.close();
         slots.clear();
     }
 
@@ -921,6 +1059,10 @@ struct azh_runner {
     }
 
     // The device-resident pass: one captured graph per batch size, replayed.
+    // A slot keeps up to kGraphsPerSlot of them (a hub's passes come in up
+    // to max_batch sizes); capturing one more first drops the one replayed
+    // least recently, after the slot's stream has finished with it.
+    static constexpr size_t kGraphsPerSlot = 64;
     void enqueuePass(Slot& s, int B) {
         if (!graphs) {
             launchPass(s, B, s.stream, shape.blocks, true);
@@ -931,6 +1073,14 @@ struct azh_runner {
         const int key = 2 * B + (useSmallTower(B) ? 1 : 0);
         auto it = s.graphs.find(key);
         if (it == s.graphs.end()) {
+            if (s.graphs.size() >= kGraphsPerSlot) {
+                auto oldest = std::min_element(s.graphs.begin(), s.graphs.end(), [](const auto& a, const auto& b) {
+                    return a.second.lastUse < b.second.lastUse;
+                });
+                check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+                check(hipGraphExecDestroy(oldest->second.exec), "hipGraphExecDestroy");
+                s.graphs.erase(oldest);
+            }
             hipGraph_t g = nullptr;
             check(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             try {
@@ -945,9 +1095,10 @@ struct azh_runner {
             const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             check(e, "hipGraphInstantiate");
-            it = s.graphs.emplace(key, exec).first;
+            it = s.graphs.emplace(key, Slot::CachedGraph{exec, 0}).first;
         }
-        check(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
+        it->second.lastUse = ++s.replays;
+        check(hipGraphLaunch(it->second.exec, s.stream), "hipGraphLaunch");
     }
 
     // The positions path's device arrays for B positions in slot s, staged
@@ -1020,53 +1171,13 @@ struct azh_runner {
               "hipMemcpyAsync(input)");
     }
     void copyOut(Slot& s, int B) {
-        const int delayUs = gCopyOutDelayUs.load();
+        const int delayUs = gHooks.copyOutDelayUs.load();
         if (delayUs > 0) check(azh::launchSpin(1000ull * delayUs, s.stream), "spin");
         check(hipMemcpyAsync(s.hLogits, s.dLogits, (size_t)B * shape.A1 * sizeof(float), hipMemcpyDeviceToHost,
                              s.stream),
               "hipMemcpyAsync(logits)");
         check(hipMemcpyAsync(s.hValues, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync(values)");
-    }
-
-    // A pass's completion: polled for up to kCompletionPollUs (a small
-    // network's pass ends within it, and the driver's wake-up from a
-    // blocking wait costs tens of microseconds), then slept on.
-    static constexpr int kCompletionPollUs = 50;
-    static hipError_t waitFor(hipEvent_t e) {
-        const auto until = std::chrono::steady_clock::now() + std::chrono::microseconds(kCompletionPollUs);
-        for (;;) {
-            const hipError_t q = hipEventQuery(e);
-            if (q != hipErrorNotReady) return q;
-            if (std::chrono::steady_clock::now() >= until) break;
-        }
-        return hipEventSynchronize(e);
-    }
-
-    void completionLoop() {
-        for (;;) {
-            Pass pass;
-            {
-                std::unique_lock<std::mutex> lock(mutex);
-                wake.wait(lock, [&] { return stop || !queue.empty(); });
-                if (queue.empty()) return;   // stopping, nothing in flight
-                pass = std::move(queue.front());
-                queue.pop_front();
-            }
-            std::string error = pass.error;
-            const hipError_t e = waitFor(slots[pass.slot]->event);
-            if (error.empty() && e != hipSuccess) error = std::string("hip: ") + hipGetErrorString(e);
-            int left = gFailCountdown.load();
-            while (left > 0 && !gFailCountdown.compare_exchange_weak(left, left - 1)) {
-            }
-            if (left == 1 && error.empty()) error = "hip: injected failure (a test hook)";
-            ++gPassesCompleted;
-            {
-                std::lock_guard<std::mutex> lock(mutex);
-                slots[pass.slot]->busy = false;
-            }
-            pass.done(pass.user, pass.slot, error.empty() ? nullptr : error.c_str());
-        }
     }
 
     Slot& slotAt(int slot) {
@@ -1080,16 +1191,13 @@ struct azh_runner {
             throw Error(AZH_ERR_ARGUMENT, "hip: batch of " + std::to_string(B) + " positions outside [1, " +
                                               std::to_string(maxBatch) + "]");
     }
-    Slot& idleSlot(int slot) {
-        Slot& s = slotAt(slot);
-        std::lock_guard<std::mutex> lock(mutex);
-        if (s.busy) throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
-        return s;
-    }
+    // The slot, held for the caller's scope (a synchronous call), or an
+    // error when a pass or another call holds it.
+    SlotClaim claimIdle(int slot) { return SlotClaim(slotAt(slot), slot); }
 };
 
 // makeCudaRunner's steps (src/cuda/cuda_runner.cu:227-234): checks, memory,
-// upload, slots, the completion thread.
+// upload, slots, then the reporter's thread.
 void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, int max_batch, int slots,
                   azh_runner** out) {
     if (!out) throw Error(AZH_ERR_ARGUMENT, "hip: no output handle");
@@ -1100,13 +1208,13 @@ void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, i
         throw Error(AZH_ERR_ARGUMENT, "makeHipRunner: slots must be in [1, " + std::to_string(kMaxSlots) + "]");
     const std::map<std::string, const float*> given = checkTensors(*cfg, tensors, count);
     requireContext();
-    checkFits((double)runnerBytes(*cfg, max_batch, slots), max_batch, 1);
+    const azh_hub_group one{1, slots, max_batch};
+    admitRunners(*cfg, &one, 1);
     std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
     uploadWeights(*cfg, given, r->weights);
     r->initTowerLayout();
     for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
-    azh_runner* raw = r.get();
-    r->completion = std::thread([raw] { raw->completionLoop(); });
+    r->reporter.start();
     *out = r.release();
 }
 
@@ -1150,21 +1258,14 @@ int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* byt
 }
 
 int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_per_hub) {
-    return guarded([&] {
-        validate(cfg);
-        if (max_batch < 1 || hubs < 1 || slots_per_hub < 1)
-            throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: bad arguments");
-        requireContext();
-        checkFits((double)hubs * runnerBytes(*cfg, max_batch, slots_per_hub), max_batch, hubs);
-    });
+    const azh_hub_group one{hubs, slots_per_hub, max_batch};
+    return azh_check_memory_groups(cfg, &one, 1);
 }
 
-int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs) {
+int azh_check_memory_groups(const azh_netcfg* cfg, const azh_hub_group* groups, int count) {
     return guarded([&] {
-        if (!(need_bytes >= 0) || max_batch < 1 || hubs < 1)
-            throw Error(AZH_ERR_ARGUMENT, "checkHipInferenceMemory: bad arguments");
-        requireContext();
-        checkFits(need_bytes, max_batch, hubs);
+        validate(cfg);
+        admitRunners(*cfg, groups, count);
     });
 }
 
@@ -1260,13 +1361,12 @@ int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user) {
         if (!r || !done) throw Error(AZH_ERR_ARGUMENT, "hip: begin needs a runner and a done callback");
         r->checkBatch(B);
         Slot& s = r->slotAt(slot);
-        {
-            std::lock_guard<std::mutex> lock(r->mutex);
-            if (s.busy) throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
-            s.busy = true;
-        }
-        // From here done is called exactly once: errors while enqueueing
-        // travel through it, as a failed pass.
+        bool idle = false;
+        if (!s.claimed.compare_exchange_strong(idle, true))
+            throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
+        // From here done is called exactly once, by the reporter, which also
+        // releases the claim: errors while enqueueing travel through it, as
+        // a failed pass.
         std::string error;
         try {
             r->copyIn(s, B);
@@ -1278,11 +1378,19 @@ int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user) {
             if (error.empty()) error = "hip: enqueue failed";
             (void)hipEventRecord(s.event, s.stream);
         }
-        {
-            std::lock_guard<std::mutex> lock(r->mutex);
-            r->queue.push_back(azh_runner::Pass{slot, done, user, std::move(error)});
+        Reporter::Notice notice;
+        notice.slot = slot;
+        notice.event = s.event;
+        notice.claim = &s.claimed;
+        notice.done = done;
+        notice.user = user;
+        notice.error = std::move(error);
+        try {
+            r->reporter.post(std::move(notice));
+        } catch (...) {
+            s.claimed.store(false);   // never handed over: no done will come
+            throw;
         }
-        r->wake.notify_all();
     });
 }
 
@@ -1291,7 +1399,8 @@ int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* va
         if (!r || !input || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: infer needs its arrays");
         if (ownership && !r->shape.ownership) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no ownership head");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(0);
+        const SlotClaim held = r->claimIdle(0);
+        Slot& s = held.slot;
         std::memcpy(s.hIn, input, (size_t)B * r->shape.P * r->shape.A * sizeof(float));
         r->copyIn(s, B);
         r->enqueuePass(s, B);
@@ -1393,7 +1502,8 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
         if (!r || !pos || !priors || !legal || !values)
             throw Error(AZH_ERR_ARGUMENT, "hip: evaluate_positions needs its arrays");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(0);
+        const SlotClaim held = r->claimIdle(0);
+        Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
         r->encodeStep(s, d, B);
         r->enqueuePass(s, B);
@@ -1415,7 +1525,8 @@ int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters
     return guarded([&] {
         if (!r || !pos || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(0);
+        const SlotClaim held = r->claimIdle(0);
+        Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
         // One untimed run of everything (the pass's graph for B is captured here).
         r->encodeStep(s, d, B);
@@ -1465,7 +1576,8 @@ int azh_stage(azh_runner* r, int slot, int B) {
     return guarded([&] {
         if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         r->copyIn(s, B);
         check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
     });
@@ -1475,7 +1587,8 @@ int azh_enqueue(azh_runner* r, int slot, int B) {
     return guarded([&] {
         if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
         r->checkBatch(B);
-        r->enqueuePass(r->idleSlot(slot), B);
+        const SlotClaim held = r->claimIdle(slot);
+        r->enqueuePass(held.slot, B);
     });
 }
 
@@ -1490,7 +1603,8 @@ int azh_fetch(azh_runner* r, int slot, int B) {
     return guarded([&] {
         if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         check(hipMemcpyAsync(s.hLogits, s.dLogits, (size_t)B * r->shape.A1 * sizeof(float),
                              hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");
@@ -1505,7 +1619,8 @@ int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms) {
     return guarded([&] {
         if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         *ms = timeOnStream(s.stream, iters, [&] { r->enqueuePass(s, B); });
     });
 }
@@ -1515,7 +1630,8 @@ int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, i
         if (!r || !ms || !launches || !layers || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         // The tower as the pass runs it: every block's two convolutions in
         // order, each reading the previous one's output.
         int per = 0;
@@ -1530,7 +1646,8 @@ int azh_time_tower_layers(azh_runner* r, int slot, int B, int iters, float* ms, 
         if (!r || !ms || !layers || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         if (r->shape.blocks < 1) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no residual block");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         *ms = timeOnStream(s.stream, iters, [&] { r->launchTowerAsPass(s, B, r->shape.blocks); });
         *layers = iters * 2 * r->shape.blocks;
     });
@@ -1540,7 +1657,8 @@ int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms) {
     return guarded([&] {
         if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(slot);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
         const auto t0 = std::chrono::steady_clock::now();
         for (int i = 0; i < iters; ++i) {
             r->copyIn(s, B);
@@ -1557,7 +1675,7 @@ int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms) {
         if (!r || !ms || passes < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         r->checkBatch(B);
         const int slots = azh_slots(r);
-        for (int i = 0; i < slots; ++i) r->idleSlot(i);
+        for (int i = 0; i < slots; ++i) r->claimIdle(i);   // each idle now (claimed and released)
         // The done handler's state outlives every pass it is handed to: all
         // of them are drained before this function returns.
         struct Done {
@@ -1709,7 +1827,8 @@ int azh_probe_heads(azh_runner* r, const float* trunk, int B, float* logits, flo
         if (!r || !trunk || !logits || !values) throw Error(AZH_ERR_ARGUMENT, "hip: bad heads probe arguments");
         if (ownership && !r->shape.ownership) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no ownership head");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(0);
+        const SlotClaim held = r->claimIdle(0);
+        Slot& s = held.slot;
         const Shape& sh = r->shape;
         const std::vector<float> tq = azh::toChannelQuads(trunk, B, sh.F, sh.A);
         check(hipMemcpyAsync(s.dX, tq.data(), tq.size() * sizeof(float), hipMemcpyHostToDevice, s.stream),
@@ -1733,7 +1852,8 @@ int azh_probe_trunk(azh_runner* r, const float* input, int B, int blocks, float*
         if (!r || !input || !trunk) throw Error(AZH_ERR_ARGUMENT, "hip: bad trunk probe arguments");
         if (blocks < 0 || blocks > r->shape.blocks) throw Error(AZH_ERR_ARGUMENT, "hip: blocks outside the network");
         r->checkBatch(B);
-        Slot& s = r->idleSlot(0);
+        const SlotClaim held = r->claimIdle(0);
+        Slot& s = held.slot;
         const Shape& sh = r->shape;
         check(hipMemcpyAsync(s.dIn, input, (size_t)B * sh.P * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
@@ -1793,11 +1913,13 @@ int azh_probe_copy(size_t bytes, int iters, float* ms) {
     });
 }
 
-void azh_set_hub_chaos_seed(uint64_t seed) { gHubChaosSeed = seed; }
-uint64_t azh_hub_chaos_seed(void) { return gHubChaosSeed.load(); }
-void azh_fail_passes_after(int n) { gFailCountdown = n > 0 ? n + 1 : 0; }
-void azh_set_memory_limit(size_t bytes) { gMemoryLimit = bytes; }
-long long azh_passes_completed(void) { return gPassesCompleted.load(); }
-void azh_set_copy_out_delay(int microseconds) { gCopyOutDelayUs = microseconds > 0 ? microseconds : 0; }
+void azh_set_hub_chaos_seed(uint64_t seed) { gHooks.hubChaosSeed.store(seed); }
+uint64_t azh_hub_chaos_seed(void) { return gHooks.hubChaosSeed.load(); }
+// The pass reported after n more have been reported fails (once); n <= 0
+// turns the injection off.
+void azh_fail_passes_after(int n) { gHooks.failingReport.store(n > 0 ? gHooks.reports.load() + n : -1); }
+void azh_set_memory_limit(size_t bytes) { gHooks.memoryLimit.store(bytes); }
+long long azh_passes_completed(void) { return gHooks.reports.load(); }
+void azh_set_copy_out_delay(int microseconds) { gHooks.copyOutDelayUs.store(std::max(microseconds, 0)); }
 
 } // extern "C"

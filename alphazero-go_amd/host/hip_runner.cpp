@@ -58,8 +58,7 @@ azh_runner* createRunner(const Network& network, int maxBatch, int slots) {
 
 class HipBatchRunner : public BatchRunner {
 public:
-    HipBatchRunner(const Network& net, int maxBatch, int slots)
-        : runner_(createRunner(net, maxBatch, slots)), done_(static_cast<size_t>(slots)) {}
+    HipBatchRunner(const Network& net, int maxBatch, int slots) : runner_(createRunner(net, maxBatch, slots)) {}
 
     // azh_destroy waits for every pass in flight (and its done) first.
     ~HipBatchRunner() override { azh_destroy(runner_); }
@@ -70,30 +69,29 @@ public:
     const float* logits(int slot) const override { return azh_slot_logits(runner_, slot); }
     const float* values(int slot) const override { return azh_slot_values(runner_, slot); }
 
-    // The slot's callback is stored before the pass starts and taken back by
-    // the completion thread, which the library calls exactly once per pass.
-    // A begin the library refuses (batch out of range, busy slot) throws and
-    // calls nothing: the hub fails the batch (src/inference_hub.cpp:237-246).
+    // Each pass carries its own callback: a heap copy handed to the library
+    // as the pass's `user`, which the library's reporter passes back exactly
+    // once (completed runs it and frees it). A begin the library refuses
+    // (batch out of range, busy slot) throws and calls nothing, and leaves
+    // any pass already in flight on the slot, and its callback, untouched:
+    // the hub fails the new batch (src/inference_hub.cpp:237-246).
     void begin(int slot, int B, std::function<void(int slot, std::string error)> done) override {
-        if (slot < 0 || slot >= static_cast<int>(done_.size()))
-            throw std::invalid_argument("hip: slot " + std::to_string(slot) + " out of range");
-        done_[static_cast<size_t>(slot)] = std::move(done);
-        const int rc = azh_begin(runner_, slot, B, &HipBatchRunner::completed, this);
+        auto* fn = new std::function<void(int, std::string)>(std::move(done));
+        const int rc = azh_begin(runner_, slot, B, &HipBatchRunner::completed, fn);
         if (rc != AZH_OK) {
-            done_[static_cast<size_t>(slot)] = nullptr;
+            delete fn;
             check(rc);
         }
     }
 
 private:
     static void completed(void* user, int slot, const char* error) {
-        auto* self = static_cast<HipBatchRunner*>(user);
-        std::function<void(int, std::string)> fn = std::move(self->done_[static_cast<size_t>(slot)]);
-        fn(slot, error ? std::string(error) : std::string());
+        std::unique_ptr<std::function<void(int, std::string)>> fn(
+            static_cast<std::function<void(int, std::string)>*>(user));
+        (*fn)(slot, error ? std::string(error) : std::string());
     }
 
     azh_runner* runner_;
-    std::vector<std::function<void(int, std::string)>> done_;
 };
 
 } // namespace
@@ -126,20 +124,11 @@ void checkHipInferenceMemory(const NetConfig& cfg, int inferenceBatch, int hubs,
 }
 
 void checkHipInferenceMemory(const NetConfig& cfg, const std::vector<GpuHubs>& groups) {
-    if (groups.empty()) throw std::invalid_argument("checkHipInferenceMemory: no hubs");
     const azh_netcfg c = toC(cfg);
-    double need = 0;
-    int hubs = 0, batch = 0;
-    for (const GpuHubs& g : groups) {
-        if (g.inferenceBatch < 1 || g.hubs < 1 || g.slotsPerHub < 1)
-            throw std::invalid_argument("checkHipInferenceMemory: bad arguments");
-        size_t bytes = 0;
-        check(azh_memory_need(&c, g.inferenceBatch, g.slotsPerHub, &bytes));
-        need += static_cast<double>(g.hubs) * static_cast<double>(bytes);
-        hubs += g.hubs;
-        batch = batch > g.inferenceBatch ? batch : g.inferenceBatch;
-    }
-    check(azh_check_memory_bytes(need, batch, hubs));
+    std::vector<azh_hub_group> g;
+    g.reserve(groups.size());
+    for (const GpuHubs& h : groups) g.push_back(azh_hub_group{h.hubs, h.slotsPerHub, h.inferenceBatch});
+    check(azh_check_memory_groups(&c, g.data(), static_cast<int>(g.size())));
 }
 
 struct HipInference::Impl {

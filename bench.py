@@ -15,6 +15,17 @@ at batch 8, as the reference bench's "cpu (blas)" row).
 
   python bench.py [--steps K] [--warmup W] [--workload 3] [--no-cpu] [--no-positions]
 
+Two more modes serve the committed profiles (each prints one line):
+
+  python bench.py --mode copy-calibration [--mib 256] [--conv-iters 5]
+      a plain device-to-device copy of known size, for scaling rocprofv3's
+      FETCH_SIZE / WRITE_SIZE readings to bytes;
+  python bench.py --mode stem-heads [--workload 3] [--batch B] [--conv-iters 10]
+      whole-batch launches of the stem convolution and the heads on one
+      stream (in a pass of a large batch they run as two concurrent
+      half-batch launches, whose traced durations overlap each other), for
+      rocprofv3 --kernel-trace.
+
 Beside the headline, "positions" times the steps either side of the pass
 (azh_evaluate_positions: encoding from stone bytes, the legal moves with
 superko, the priors) on the same boards, each position carrying 200
@@ -58,6 +69,8 @@ def parse():
     ap.add_argument("--no-two-slot", action="store_true",
                     help="skip the runner-kept-full rate (its two slots overlap kernels; for kernel-trace profiles)")
     ap.add_argument("--seen", type=int, default=200, help="superko hashes per position")
+    ap.add_argument("--mode", default="pass", choices=["pass", "copy-calibration", "stem-heads"])
+    ap.add_argument("--mib", type=int, default=256, help="copy-calibration: MiB copied per launch")
     return ap.parse_args()
 
 
@@ -81,16 +94,37 @@ def traffic_from_profile(workload_name, kernel_hash, kernel):
         return None
 
 
+def host_cpus():
+    """The host's CPUs as this process sees them: the affinity set, the
+    machine's count, and the container's CPU quota (cgroup v2 cpu.max) when
+    one is set."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()
+            if q != "max":
+                quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    return {"affinity": affinity, "cpu_count": os.cpu_count(), "cgroup_quota": quota}
+
+
 def cpu_baseline(workload, calls):
     """The oracle's blas pass (im2col + single-threaded OpenBLAS sgemm, the
-    reference's CPU backend restated) on this host: one worker per core, each
-    running `calls` passes of batch 8, plus one batch-256 pass on one worker."""
+    reference's CPU backend restated) on this host: one worker per CPU the
+    process may run on (the affinity set, within the container's CPU quota),
+    each running `calls` passes of batch 8 (the reference bench's "cpu
+    (blas)" row, apps/bench.cpp:452-476), plus one batch-256 pass on one
+    worker."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     w = O.WORKLOADS[workload]
     net = O.init_network(w.cfg)
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    workers = max(1, min(16, cores))
+    host = host_cpus()
+    workers = host["affinity"]
+    if host["cgroup_quota"]:
+        workers = max(1, min(workers, int(host["cgroup_quota"])))
     inp8, _ = O.workload_inputs(w, 8)
     rate, elapsed = O.time_workers(net, inp8, workers, calls, O.BLAS)
     one_b = min(w.batch, 256)
@@ -100,14 +134,50 @@ def cpu_baseline(workload, calls):
         "value": round(rate, 2),
         "unit": "positions/s",
         "cores": workers,
+        "host_cpus": host,
         "kind": "port",
-        "sample": f"{workers} workers x {calls} passes of batch 8 ({workers * calls * 8} positions, "
-                  f"{elapsed:.1f} s); oracle blas restatement of Network::infer",
+        "sample": f"{workers} single-threaded workers (one per host CPU) x {calls} passes of batch 8 "
+                  f"({workers * calls * 8} positions, {elapsed:.1f} s); oracle blas restatement of Network::infer",
         "single_worker_batch": one_b,
         "single_worker_seconds": round(el_one, 2),
         "single_worker_value": round(rate_one, 2),
         "blas": O.blas_description(),
     }
+
+
+def copy_calibration(mib, iters):
+    """A plain device copy of known size: FETCH_SIZE and WRITE_SIZE per
+    dispatch against the bytes moved give the counters' scale factors."""
+    import azgo_hip
+    nbytes = mib << 20
+    ms = azgo_hip.probe_copy(nbytes, iters)
+    print(json.dumps({"mode": "copy-calibration", "bytes_per_copy": nbytes, "copies": iters,
+                      "ms_per_copy": round(ms / iters, 4),
+                      "gb_s_read_plus_write": round(2 * nbytes / (ms / iters * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def stem_heads(workload, B, iters):
+    """Whole-batch launches of the heads (on a trunk uploaded before each)
+    and of the stem convolution (the input planes to F channels, the
+    batch's workgroup shape) on one stream, random weights with BN
+    variances in [0.5, 1.5]."""
+    import numpy as np
+    import azgo_hip
+    import workload as W
+    w = W.WORKLOADS[workload]
+    B = B or w.batch
+    n, H, blocks, F, V = w.cfg
+    cfg = azgo_hip.net_cfg(n, H, blocks, F, V)
+    rng = np.random.default_rng(1)
+    tensors = {name: rng.uniform(*((0.5, 1.5) if name.endswith("runVar") else (-0.05, 0.05)), floats)
+               .astype(np.float32) for name, floats in azgo_hip.tensor_spec(cfg)}
+    with azgo_hip.Runner(cfg, tensors, B, 1) as r:
+        trunk = rng.uniform(0, 2, (B, F, n * n)).astype(np.float32)
+        for _ in range(iters):
+            r.probe_heads(trunk)
+    ms = azgo_hip.time_conv3x3(B, n, cfg.planes, F, -1, iters)
+    print(json.dumps({"mode": "stem-heads", "workload": f"{n}x{n} {blocks}x{F} batch {B}", "head_launches": iters,
+                      "stem_us_per_launch": round(ms / iters * 1e3, 2)}), flush=True)
 
 
 def positions_leg(r, w, B, seen_per_position, iters=20):
@@ -178,6 +248,10 @@ def main():
     ok, why = azgo_hip.available()
     if not ok:
         raise SystemExit(f"bench.py: no usable gfx950 GPU: {why}")
+    if args.mode == "copy-calibration":
+        return copy_calibration(args.mib, args.conv_iters)
+    if args.mode == "stem-heads":
+        return stem_heads(args.workload, args.batch, args.conv_iters)
     w = W.WORKLOADS[args.workload]
     B = args.batch or w.batch
     n, H, blocks, F, V = w.cfg
@@ -219,6 +293,16 @@ def main():
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
         rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
         rt_median_ms = statistics.median(r.time_round_trips(0, B, 1) for _ in range(max(3, args.steps // 5)))
+        # The first pass at a batch size the slot has not run (its graph is
+        # captured and instantiated then), against the same size once cached.
+        capture = None
+        if B > 1:
+            new_b = B - 1
+            first_ms = r.time_round_trips(0, new_b, 1)
+            cached_ms = statistics.median(r.time_round_trips(0, new_b, 1) for _ in range(3))
+            capture = {"batch": new_b, "first_round_trip_ms": round(first_ms, 4),
+                       "cached_round_trip_ms": round(cached_ms, 4),
+                       "capture_ms": round(first_ms - cached_ms, 4)}
         # Both slots kept full through begin/done, each pass with its own
         # pinned copies (the reference bench's "2-slot" GPU rate).
         two_slot = None
@@ -250,7 +334,11 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(value / REFERENCE_POS_PER_S, 3) if args.workload == 3 and B == 256 else None,
+        # The reference's figure includes the pinned copies (both slots kept
+        # full, apps/bench.cpp:227-279): compared with this build's rate
+        # measured the same way, not with the device-resident `value`.
+        "vs_baseline": (round(two_slot / REFERENCE_POS_PER_S, 3)
+                        if args.workload == 3 and B == 256 and two_slot else None),
         "dtype": "fp32",
         "data": "synthetic (seeded He-normal weights, synthetic BN statistics, random boards)",
         "config": {"workload": name, "board": n, "blocks": blocks, "filters": F, "value_hidden": V,
@@ -262,6 +350,7 @@ def main():
         "round_trip_ms": round(rt_ms, 4),
         "round_trip_median_ms": round(rt_median_ms, 4),
         "two_slot_positions_per_s": two_slot,
+        "new_batch_size": capture,
         "roofline": {
             "kernel": kernel_name,
             "bound": "mfma",

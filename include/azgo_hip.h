@@ -98,11 +98,20 @@ int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* byt
  * 512 MB (or the test hook's limit). */
 int azh_check_memory(const azh_netcfg* cfg, int max_batch, int hubs, int slots_per_hub);
 
-/* The same check for a total already summed over several groups of hubs
- * (checkCudaInferenceMemory's overload over GpuHubs groups,
- * src/cuda/cuda_runner.cu:242-256): need_bytes against free memory less
- * 512 MB; max_batch and hubs only word the message. */
-int azh_check_memory_bytes(double need_bytes, int max_batch, int hubs);
+/* GpuHubs (include/azgo/gpu_memory.hpp): `hubs` runners of `slots_per_hub`
+ * slots of up to max_batch positions each. */
+typedef struct azh_hub_group {
+    int hubs;
+    int slots_per_hub;
+    int max_batch;
+} azh_hub_group;
+
+/* checkCudaInferenceMemory's overload over groups of hubs
+ * (include/azgo/cuda.hpp:63-66; src/cuda/cuda_runner.cu:242-256): every
+ * group's runners summed, against free memory less 512 MB. The refusal
+ * names the total hub count and the largest max_batch. No group, or a
+ * group with a count below 1, is AZH_ERR_ARGUMENT. */
+int azh_check_memory_groups(const azh_netcfg* cfg, const azh_hub_group* groups, int count);
 
 /* makeCudaRunner (include/azgo/cuda.hpp:53-58; src/cuda/cuda_runner.cu:227-234)
  * and CudaWeights::upload (src/cuda/cuda_network.cu:71-106): checks memory,

@@ -820,8 +820,28 @@ static const float* tensor(const azo_entry* e, int n, const float* params, const
  * mode 0 = naive backend, 1 = blas. Returns 0, or -2 when blas is not
  * loadable, -1 when out of memory.
  */
+static int forward_impl(const azo_cfg* c, const float* params, const float* buffers, const float* input, int B,
+                        int mode, int blocks, float* trunk_out, float* logits, float* values, float* ownership);
+
 int azo_forward(const azo_cfg* c, const float* params, const float* buffers, const float* input, int B, int mode,
                 float* logits, float* values, float* ownership) {
+    return forward_impl(c, params, buffers, input, B, mode, c->blocks, NULL, logits, values, ownership);
+}
+
+/*
+ * The trunk alone: the stem and the first `blocks` residual blocks of
+ * Network::forward (src/network.cpp:241-272), the same arithmetic as
+ * azo_forward, returned batch-major as trunk [B][F][A] (the network keeps it
+ * channel-major, [F][B][A]).
+ */
+int azo_trunk(const azo_cfg* c, const float* params, const float* buffers, const float* input, int B, int mode,
+              int blocks, float* trunk) {
+    if (blocks < 0 || blocks > c->blocks) return -3;
+    return forward_impl(c, params, buffers, input, B, mode, blocks, trunk, NULL, NULL, NULL);
+}
+
+static int forward_impl(const azo_cfg* c, const float* params, const float* buffers, const float* input, int B,
+                        int mode, int blocks, float* trunk_out, float* logits, float* values, float* ownership) {
     azo_entry e[AZO_MAX_ENTRIES];
     size_t pf, bf;
     const int ne = build_layout(c, e, &pf, &bf);
@@ -856,7 +876,7 @@ int azo_forward(const azo_cfg* c, const float* params, const float* buffers, con
     NORM("stem.bn", F, convOut, x);
     relu(x, trunk);
     /* Blocks: conv -> BN -> ReLU -> conv -> BN -> + input -> ReLU (:259-272). */
-    for (int i = 0; i < c->blocks; ++i) {
+    for (int i = 0; i < blocks; ++i) {
         char pre[64], nm[96];
         snprintf(pre, sizeof pre, "block%d", i);
         snprintf(nm, sizeof nm, "%s.conv1.w", pre);
@@ -885,6 +905,12 @@ int azo_forward(const azo_cfg* c, const float* params, const float* buffers, con
         float* t = x;
         x = out;
         out = t;
+    }
+    if (trunk_out) {
+        for (int ch = 0; ch < F; ++ch)
+            for (int b = 0; b < B; ++b)
+                memcpy(trunk_out + ((size_t)b * F + ch) * A, x + ((size_t)ch * B + b) * A, sizeof(float) * A);
+        goto done;
     }
     /* Policy head: 1x1 conv F -> 2, BN, ReLU, flatten c*A + p, Linear (:274-286). */
     if ((rc = gemm(mode, 0, 2, (int)M, F, T("policy.conv.w"), x, convOut))) goto done;

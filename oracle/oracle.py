@@ -117,6 +117,7 @@ def _lib():
         h.azo_conv3x3.argtypes = [C.c_int, f32, C.c_int, C.c_int, f32, C.c_int, C.c_int, f32, f32]
         h.azo_gemm.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, f32, f32, f32]
         h.azo_forward.argtypes = [P(Cfg), f32, f32, f32, C.c_int, C.c_int, f32, f32, f32]
+        h.azo_trunk.argtypes = [P(Cfg), f32, f32, f32, C.c_int, C.c_int, C.c_int, f32]
         h.azo_forward_double.argtypes = [P(Cfg), f32, f32, f32, C.c_int, f32, f32, f32]
         h.azo_softmax_legal.argtypes = [f32, u8, C.c_int, C.c_int, f32]
         u64p = P(C.c_uint64)
@@ -303,6 +304,37 @@ def forward(net: Net, inp, mode=BLAS, ownership=False):
     if rc != 0:
         raise RuntimeError(f"oracle forward failed ({rc})")
     return (logits, values, own) if ownership else (logits, values)
+
+
+def trunk(net: Net, inp, blocks=None, mode=BLAS):
+    """The stem and the first `blocks` residual blocks (all by default) of
+    the forward pass, [B][F][A]: the arithmetic of forward()."""
+    cfg = net.cfg
+    inp = _f32(inp)
+    B = inp.shape[0]
+    blocks = cfg.blocks if blocks is None else blocks
+    out = np.empty((B, cfg.filters, cfg.area), np.float32)
+    rc = _lib().azo_trunk(C.byref(cfg), fptr(net.params), fptr(net.buffers), fptr(inp), B, mode, blocks, fptr(out))
+    if rc == -2:
+        raise RuntimeError("oracle: no CBLAS library could be loaded")
+    if rc != 0:
+        raise RuntimeError(f"oracle trunk failed ({rc})")
+    return out
+
+
+def threaded(fn, inp, chunk, workers=None):
+    """fn over inp in chunks of `chunk` positions on a pool of threads (the
+    oracle's passes are single-threaded C calls that release the
+    interpreter), concatenated in order: one position's outputs depend on
+    its own input only."""
+    from concurrent.futures import ThreadPoolExecutor
+    workers = workers or max(1, min(16, len(os.sched_getaffinity(0))))
+    parts = [inp[i:i + chunk] for i in range(0, len(inp), chunk)]
+    with ThreadPoolExecutor(workers) as ex:
+        outs = list(ex.map(fn, parts))
+    if isinstance(outs[0], tuple):
+        return tuple(np.concatenate([o[k] for o in outs]) for k in range(len(outs[0])))
+    return np.concatenate(outs)
 
 
 def forward_double(net: Net, inp, ownership=False):

@@ -26,6 +26,16 @@ Vectors (data only, no reference source):
                   head (version 2)
   gen0_infer.npz  Network::infer of those two checkpoints as loadNetwork
                   reads them, on the 5x5 workload's batch of 8 positions
+  trunk.npz       the trunk (stem and the first k residual blocks,
+                  src/network.cpp:241-272) of the reference's Network::infer,
+                  read out through its own policy head made an exact copy:
+                  a one-hot 1x1 conv row picks channel c, the batch norm is
+                  the identity (gamma 1, beta 0, mean 0, runVar 1 - 1e-5,
+                  whose scale rounds to exactly 1), the ReLU passes the
+                  trunk's nonnegative values, and an identity Linear with
+                  zero bias copies the A points into the first A logits; for
+                  the 5x5 4x32 workload network (k = 0, 2, 4) and a 9x9 2x16
+                  network with random BN and biases (k = 2)
   games.npz       random games played by the reference's Game with
                   bnCalibrationPositions' move choice (src/bn_calibration.cpp:19-28):
                   every position's stones, side to move, Board::hash and the
@@ -109,9 +119,54 @@ def main():
     tensors = {"t_" + k: v for k, v in net.tensors().items()}
     np.savez_compressed(os.path.join(HERE, "infer_9x9_random.npz"), input=inp, logits=logits, values=values,
                         **tensors)
+    trunks()
     calibrated()
     games()
     print("golden vectors written to", HERE)
+
+
+def reference_trunk(net, inp, blocks):
+    """The reference's trunk after `blocks` blocks, [B][F][A], one channel
+    per Network::infer through a policy head made an exact copy."""
+    cfg = O.make_cfg(net.cfg.board, blocks, net.cfg.filters, net.cfg.value_hidden, net.cfg.history)
+    ref = O.RefNetwork(cfg, 1)
+    names = {name for name, _, _, _ in ref.layout()}
+    for name, t in net.tensors().items():
+        if name in names and not name.startswith("policy."):
+            ref.set(name, t)
+    F, A = cfg.filters, cfg.area
+    ref.set("policy.bn.gamma", np.ones(2, np.float32))
+    ref.set("policy.bn.beta", np.zeros(2, np.float32))
+    ref.set("policy.bn.runMean", np.zeros(2, np.float32))
+    ref.set("policy.bn.runVar", np.full(2, 1 - 1e-5, np.float32))
+    assert np.float32(1) / np.sqrt(np.float32(1 - 1e-5) + np.float32(1e-5)) == 1
+    fc = np.zeros((A + 1, 2 * A), np.float32)
+    fc[np.arange(A), np.arange(A)] = 1
+    ref.set("policy.fc.w", fc)
+    ref.set("policy.fc.b", np.zeros(A + 1, np.float32))
+    out = np.empty((inp.shape[0], F, A), np.float32)
+    for c in range(F):
+        w = np.zeros((2, F), np.float32)
+        w[0, c] = 1
+        ref.set("policy.conv.w", w)
+        out[:, c] = ref.infer(inp)[0][:, :A]
+    return out
+
+
+def trunks():
+    res = {}
+    w = O.WORKLOADS[1]
+    net = O.init_network(w.cfg)
+    inp, _ = O.workload_inputs(w, 8)
+    res["5x5/input"] = inp
+    for k in (0, 2, 4):
+        res[f"5x5/trunk{k}"] = reference_trunk(net, inp, k)
+    cfg = O.make_cfg(9, 2, 16, value_hidden=16)
+    net = O.random_network(cfg, 9)
+    inp = np.random.default_rng(10).integers(0, 2, (3, cfg.planes, cfg.area)).astype(np.float32)
+    res["9x9/input"] = inp
+    res["9x9/trunk2"] = reference_trunk(net, inp, 2)
+    np.savez_compressed(os.path.join(HERE, "trunk.npz"), **res)
 
 
 # (board size, seeds, moves): lengths reach captures, ko fights (superko
@@ -167,6 +222,8 @@ def calibrated():
 if __name__ == "__main__":
     if sys.argv[1:] == ["calibrated"]:
         calibrated()
+    elif sys.argv[1:] == ["trunks"]:
+        trunks()
     elif sys.argv[1:] == ["games"]:
         games()
     else:

@@ -251,6 +251,29 @@ void refusals() {
         threw = true;
     }
     expect(threw, "a batch above maxBatch refused at begin, without a done call");
+
+    // A begin on a slot whose pass is still in flight (held by the copy-out
+    // delay) is refused and calls nothing; the pass in flight keeps its own
+    // callback, which runs exactly once.
+    std::atomic<int> firstCalls{0}, secondCalls{0};
+    std::string firstError = "unset";
+    hip_probe::setCopyOutDelay(100000);
+    r->begin(0, 4, [&](int, std::string err) {
+        firstError = err;
+        ++firstCalls;
+    });
+    threw = false;
+    try {
+        r->begin(0, 4, [&](int, std::string) { ++secondCalls; });
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("in flight") != std::string::npos;
+    }
+    hip_probe::setCopyOutDelay(0);
+    expect(threw, "a begin on a busy slot refused, naming the pass in flight");
+    for (int i = 0; i < 2000 && firstCalls.load() == 0; ++i) std::this_thread::sleep_for(std::chrono::milliseconds(1));
+    std::this_thread::sleep_for(std::chrono::milliseconds(20));
+    expect(firstCalls.load() == 1 && firstError.empty(), "the pass in flight reported once, without error");
+    expect(secondCalls.load() == 0, "the refused begin's callback never ran");
 }
 
 // The destructor waits for passes in flight (src/cuda/cuda_runner.cu:64-71),

@@ -140,6 +140,17 @@ def test_runner_argument_checks():
         assert e.value.code == azgo_hip.ERR_ARGUMENT
 
 
+def test_memory_groups_refused_before_any_device_work():
+    """No group, or a group with a count below 1, is an argument error
+    (checkCudaInferenceMemory's "no hubs" / "bad arguments"), found on the host."""
+    cfg = to_hip_cfg(azgo_hip, O.WORKLOADS[1].cfg)
+    for groups in ([], [(1, 2, 0)], [(0, 2, 8)], [(1, 0, 8)], [(1, 2, 8), (1, 1, -1)]):
+        with pytest.raises(azgo_hip.HipError) as e:
+            azgo_hip.check_memory_groups(cfg, groups)
+        assert e.value.code == azgo_hip.ERR_ARGUMENT, groups
+        assert "checkHipInferenceMemory" in str(e.value)
+
+
 def test_hooks_round_trip():
     azgo_hip.set_hub_chaos_seed(12345)
     assert azgo_hip.hub_chaos_seed() == 12345

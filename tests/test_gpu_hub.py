@@ -24,15 +24,15 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DRIVER = os.path.join(ROOT, "oracle", "_ref", "hub_hip_driver")
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skipif(not os.path.exists(DRIVER),
-                       reason="hub driver not built: it compiles the reference's sources (make -C oracle hubdriver)"),
-]
+pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain", "ownership", "throughput"])
 def test_reference_hub_drives_hip_runner(hip, scenario):
+    # The driver is built beside the library (make -C oracle, from the
+    # reference's sources): a library without it is an incomplete build, not
+    # a reason to skip the drop-in proof.
+    assert os.path.exists(DRIVER), f"{DRIVER} missing: build it with `make -C oracle hubdriver`"
     r = subprocess.run([DRIVER, scenario], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr

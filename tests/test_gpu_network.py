@@ -10,6 +10,7 @@ properties: batch independence and repeatability, bit for bit.
 """
 import os
 import threading
+import time
 
 import numpy as np
 import pytest
@@ -63,6 +64,16 @@ def test_benchmark_workload_parity(hip, tag, B):
     assert rep["argmax_agree"] >= 0.999, rep
     if rep["max_abs_logit"] < 100:   # 1e-4 is above a few ulp of every logit
         assert rep["logits_maxabs"] <= 1e-4 and rep["values_maxabs"] <= 1e-4, rep
+    if rep["max_abs_logit"] == 0:
+        # Degenerate outputs (the 19x19 10x128 network with the synthetic BN
+        # statistics: every policy pre-activation is negative, every logit the
+        # zero bias, every value -1) show nothing of the trunk: compare it.
+        with _runner(hip, net, B) as r:
+            trunk = r.probe_trunk(inp, w.cfg.blocks)
+        ref = O.trunk(net, inp, mode=O.BLAS)
+        err = O.max_err(trunk, ref)
+        print(f"workload {tag} B={B}: degenerate outputs; trunk maxErr {err:.3g} (max {ref.max():.4g})")
+        assert ref.max() > 10 and err <= 1e-5, err
 
 
 def test_wide_net_vs_double(hip):
@@ -174,6 +185,24 @@ def test_every_batch_size_equals_singles(hip):
             got = r.infer(inp[:B])
             for i in range(B):
                 assert bitwise_equal(got[0][i], alone[i][0][0]) and bitwise_equal(got[1][i], alone[i][1][0]), (B, i)
+
+
+def test_graph_cache_eviction_keeps_the_bits(hip):
+    """A slot keeps at most 64 captured passes: 80 batch sizes in turn evict
+    the least recently replayed ones, and a size captured again after its
+    eviction (and one still cached) gives the same bits as before."""
+    w = O.WORKLOADS[1]
+    net = O.random_network(w.cfg, 608)
+    inp, _ = O.workload_inputs(w, 80)
+    with _runner(hip, net, 80, slots=1) as r:
+        first = {B: r.infer(inp[:B]) for B in (1, 2, 3)}
+        for B in range(4, 81):
+            got = r.infer(inp[:B])
+            assert np.isfinite(got[0]).all()
+        for B in (1, 2, 3, 80):   # 1-3 were evicted, 80 is the newest
+            again = r.infer(inp[:B])
+            want = first.get(B, got)
+            assert bitwise_equal(again[0], want[0]) and bitwise_equal(again[1], want[1]), B
 
 
 @pytest.mark.parametrize("B", [5, 6, 8, 9, 16, 17, 18, 28, 29, 32, 33, 34, 115, 116, 128, 129, 217, 218])
@@ -558,6 +587,58 @@ def test_runner_rejects_bad_begin(hip):
             with pytest.raises(hip.HipError) as e:
                 r.begin(slot, B, lambda s, err: None)
             assert e.value.code == hip.ERR_ARGUMENT
+
+
+def test_busy_slot_refusal_keeps_the_pass_in_flight(hip):
+    """A begin on a slot whose pass is still in flight (held by the copy-out
+    delay) is refused with a state error and calls nothing, and so is a
+    synchronous call on that slot; the first pass's done still comes exactly
+    once, with the synchronous pass's bits."""
+    w = O.WORKLOADS[1]
+    net = O.init_network(w.cfg)
+    inp, _ = O.workload_inputs(w, 8)
+    with _runner(hip, net, 8, slots=1) as r:
+        sync = r.infer(inp)
+        r.input(0)[:8] = inp
+        calls = []
+        ev = threading.Event()
+        hip.set_copy_out_delay(200000)
+        try:
+            r.begin(0, 8, lambda s, e: (calls.append(e), ev.set()))
+            with pytest.raises(hip.HipError) as e1:
+                r.begin(0, 8, lambda s, e: calls.append("second"))
+            with pytest.raises(hip.HipError) as e2:
+                r.infer(inp)
+        finally:
+            hip.set_copy_out_delay(0)
+        assert e1.value.code == hip.ERR_STATE and e2.value.code == hip.ERR_STATE
+        assert ev.wait(30)
+        time.sleep(0.05)
+        assert calls == [None]
+        assert bitwise_equal(r.logits(0, 8), sync[0]) and bitwise_equal(r.values(0, 8), sync[1])
+
+
+def test_memory_check_groups(hip):
+    """checkCudaInferenceMemory's overload over GpuHubs groups
+    (src/cuda/cuda_runner.cu:242-256): the groups are summed, the refusal
+    names every hub and the largest batch, and the sum of two groups equals
+    the memory of their runners."""
+    cfg = to_hip_cfg(hip, O.WORKLOADS[3].cfg)
+    hip.set_memory_limit(1 << 20)
+    try:
+        with pytest.raises(hip.HipError) as e:
+            hip.check_memory_groups(cfg, [(1, 2, 256), (2, 1, 64)])
+        msg = str(e.value)
+        assert e.value.code == hip.ERR_MEMORY and "(3 hubs)" in msg and "inference_batch 256" in msg
+        need = hip.memory_need(cfg, 256, 2) + 2 * hip.memory_need(cfg, 64, 1)
+        assert f"needs {need // 10**6} MB" in msg
+        hip.set_memory_limit(need)
+        hip.check_memory_groups(cfg, [(1, 2, 256), (2, 1, 64)])   # exactly fits
+        hip.set_memory_limit(need - 1)
+        with pytest.raises(hip.HipError):
+            hip.check_memory_groups(cfg, [(1, 2, 256), (2, 1, 64)])
+    finally:
+        hip.set_memory_limit(0)
 
 
 def test_memory_check_message(hip):

@@ -352,11 +352,30 @@ def test_softmax_closed_forms():
     assert np.allclose(p[2], 0.25)
 
 
+def test_trunk_equals_reference_build():
+    """The oracle's trunk (the stem and the first k blocks, what the GPU's
+    trunk probe returns) equals the reference's own Network::infer's trunk
+    bit for bit, read out of the reference build through a policy head made
+    an exact copy (tests/golden/trunk.npz): the 5x5 workload network at
+    depths 0, 2 and 4, and a 9x9 network with random BN and biases."""
+    g = np.load(os.path.join(GOLD, "trunk.npz"))
+    net = O.init_network(O.WORKLOADS[1].cfg)
+    for k in (0, 2, 4):
+        got = O.trunk(net, g["5x5/input"], k, mode=O.NAIVE)
+        assert np.array_equal(_bits(got), _bits(g[f"5x5/trunk{k}"])), k
+    net = O.random_network(O.make_cfg(9, 2, 16, value_hidden=16), 9)
+    assert np.array_equal(_bits(O.trunk(net, g["9x9/input"], 2, mode=O.NAIVE)), _bits(g["9x9/trunk2"]))
+    # The blas trunk is the same computation up to the gemm's summation order.
+    blas = O.trunk(net, g["9x9/input"], 2, mode=O.BLAS)
+    assert O.max_err(blas, g["9x9/trunk2"]) <= 1e-6
+
+
 def test_workload_generator_equals_oracle():
     """The benchmark's own generator (alphazero-go_amd/workload) produces the
-    oracle's tensors and positions bit for bit."""
+    oracle's tensors and positions bit for bit, for every workload (4 is
+    3's network at its small batches)."""
     import workload as W
-    for tag in (1, 2):
+    for tag in (1, 2, 3, 4, 5):
         w, ow = W.WORKLOADS[tag], O.WORKLOADS[tag]
         t, ot = W.network_tensors(w.cfg), O.init_network(ow.cfg).tensors()
         assert list(t) == list(ot)
