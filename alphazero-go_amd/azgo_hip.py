@@ -94,6 +94,7 @@ def load():
             "azh_slot_values": ([vp, C.c_int], f32),
             "azh_begin": ([vp, C.c_int, C.c_int, DONE_FN, vp], C.c_int),
             "azh_infer": ([vp, f32, C.c_int, f32, f32, f32], C.c_int),
+            "azh_infer_noalloc": ([vp, vp, C.c_int, vp, vp, vp, vp], C.c_int),
             "azh_softmax_legal": ([f32, u8, C.c_int, C.c_int, f32], C.c_int),
             "azh_encode_planes": ([u8, P(C.c_int32), u8, u8, C.c_int, C.c_int, C.c_int, f32], C.c_int),
             "azh_legal_moves": ([u8, C.c_int, u8, P(C.c_uint64), P(C.c_int64), C.c_int, u8], C.c_int),
@@ -440,6 +441,14 @@ class Runner:
         own = np.empty((B, self.cfg.board * self.cfg.board), np.float32) if ownership else None
         _check(self.lib.azh_probe_heads(self.h, _f(trunk), B, _f(logits), _f(values), _f(own) if ownership else None))
         return (logits, values, own) if ownership else (logits, values)
+
+    def infer_noalloc(self, d_input, B, d_logits, d_values, d_ownership=None, stream=None):
+        """The pass on device arrays (integer device addresses) enqueued on
+        `stream` (an integer hipStream_t, None: the null stream), allocating
+        nothing; the caller synchronizes."""
+        _check(self.lib.azh_infer_noalloc(self.h, C.c_void_p(d_input), B, C.c_void_p(d_logits),
+                                          C.c_void_p(d_values), C.c_void_p(d_ownership) if d_ownership else None,
+                                          C.c_void_p(stream) if stream else None))
 
     def probe_trunk(self, inp, blocks):
         inp = _f32(inp)

@@ -154,6 +154,42 @@ void requireContext() {
     if (!c.ok) throw Error(AZH_ERR_UNAVAILABLE, "hip: no usable GPU (" + c.why + ")");
 }
 
+} // namespace
+
+// ---------------------------------------------------------------- the allocation-free pass's scratch
+
+// The device memory azh_infer_noalloc works in (the trunk, the blocks'
+// middle activations and the heads' rows; 256 boards of 19x19 at 128
+// channels take 91.3 MiB of it): one array per device, there from the
+// library's load until the process ends, shared by every such call on that
+// device. Host code never hands the name `scratch` to a kernel (on the host
+// it is only a stand-in for the symbol): it uses the device address that
+// scratchOnCurrentDevice resolved.
+constexpr size_t kScratchBytes = size_t(96) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> gScratchByDevice[kMaxDevices];   // null until resolved
+std::mutex gScratchResolve;
+
+// The scratch array's address on the current device, resolved (with that
+// device current) the first time, then read without a lock.
+float* scratchOnCurrentDevice() {
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw Error(AZH_ERR_UNAVAILABLE, "hip: device index above 63");
+    if (float* p = gScratchByDevice[dev].load(std::memory_order_acquire)) return p;
+    std::lock_guard<std::mutex> lock(gScratchResolve);
+    if (float* p = gScratchByDevice[dev].load(std::memory_order_acquire)) return p;
+    void* p = nullptr;
+    check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) throw Error(AZH_ERR_HIP, "hip: the scratch array has no device address");
+    gScratchByDevice[dev].store(static_cast<float*>(p), std::memory_order_release);
+    return static_cast<float*>(p);
+}
+
 // ---------------------------------------------------------------- network shape
 
 struct Shape {
@@ -503,6 +539,13 @@ size_t slotFloats(const Shape& s, int maxBatch) {
            alignFloats(B * s.A1) + alignFloats(B) + (s.ownership ? alignFloats(B * s.A) : 0);
 }
 
+// Floats of scratch an allocation-free pass of B boards takes: the trunk and
+// the middle activations in channel quads, then the heads' rows, each
+// 256-byte aligned.
+size_t noallocScratchFloats(const Shape& sh, int B) {
+    return 2 * alignFloats(azh::quadFloats(B, sh.F, sh.A)) + alignFloats((size_t)B * 3 * sh.A);
+}
+
 size_t runnerBytes(const azh_netcfg& c, int maxBatch, int slots) {
     return (size_t)slots * slotFloats(Shape(c), maxBatch) * sizeof(float) + weightFloats(c) * sizeof(float);
 }
@@ -849,6 +892,7 @@ struct azh_runner {
     } tower;
 
     Reporter reporter;
+    int device = 0;   // where the weights and slots live
 
     azh_runner(const azh_netcfg& c, int mb) : cfg(c), shape(c), maxBatch(mb) {}
 
@@ -883,41 +927,54 @@ struct azh_runner {
         return launchTowerOn(s.dX, s.dMid, B, azh::chooseConvTiling(shape.F, B, shape.n), stream, blocksToRun);
     }
 
-    // Boards [b0, b0 + Bp) of slot s's pass on `stream`: the stem,
-    // `blocksToRun` residual blocks, then the heads when asked; workgroup
-    // shape t (the shape decides only which workgroup computes an output,
-    // never how, so a part's bits are the whole batch's).
-    void launchPassPart(Slot& s, int b0, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun,
-                        bool heads, bool small) {
+    // Where a pass over Bp boards reads and writes: the input planes
+    // [Bp][P][A], the trunk and the blocks' middle activations (channel
+    // quads), the heads' rows [Bp][3][A], and the outputs (own may be null:
+    // no ownership).
+    struct PassBuffers {
+        const float* in;
+        float *x, *mid, *act, *logits, *values, *own;
+    };
+    // Slot s's buffers from board b0 on.
+    PassBuffers slotBuffers(Slot& s, int b0) const {
         const Shape& sh = shape;
         const size_t trunk = azh::quadFloats(1, sh.F, sh.A);   // floats per board
-        float* x = s.dX + b0 * trunk;
-        float* mid = s.dMid + b0 * trunk;
+        return PassBuffers{s.dIn + (size_t)b0 * sh.P * sh.A,  s.dX + b0 * trunk,
+                           s.dMid + b0 * trunk,               s.dAct + (size_t)b0 * 3 * sh.A,
+                           s.dLogits + (size_t)b0 * sh.A1,    s.dValues + b0,
+                           s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr};
+    }
+
+    // A pass over Bp boards on `stream`: the stem, `blocksToRun` residual
+    // blocks, then the heads when asked; workgroup shape t (the shape
+    // decides only which workgroup computes an output, never how, so a
+    // part's bits are the whole batch's).
+    void launchPassPart(const PassBuffers& io, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun,
+                        bool heads, bool small) {
+        const Shape& sh = shape;
         if (small) {
             // The stem, the tower and the heads in one launch.
-            const azh::SmallStem stem{s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
-                                      weights.stem.shift, sh.P};
+            const azh::SmallStem stem{io.in, weights.stem.w, weights.stem.scale, weights.stem.shift, sh.P};
             azh::SmallHeads hd;
             if (heads) {
                 hd.w = weights.heads;
-                hd.logits = s.dLogits + (size_t)b0 * sh.A1;
-                hd.values = s.dValues + b0;
-                hd.own = s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr;
+                hd.logits = io.logits;
+                hd.values = io.values;
+                hd.own = io.own;
                 hd.V = sh.V;
             }
-            check(azh::launchSmallTower(x, &stem, &hd, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
+            check(azh::launchSmallTower(io.x, &stem, &hd, tower.w0, tower.stride, tower.scaleOff, tower.shiftOff,
                                         2 * std::max(blocksToRun, 0), Bp, sh.n, sh.F, stream),
                   "small-board pass");
             return;
         }
-        check(azh::launchConv3x3(s.dIn + (size_t)b0 * sh.P * sh.A, weights.stem.w, weights.stem.scale,
-                                 weights.stem.shift, nullptr, x, Bp, sh.n, sh.P, sh.F, true, true, t, stream),
+        check(azh::launchConv3x3(io.in, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, io.x, Bp,
+                                 sh.n, sh.P, sh.F, true, true, t, stream),
               "conv3x3 (stem)");
-        launchTowerOn(x, mid, Bp, t, stream, blocksToRun);
+        launchTowerOn(io.x, io.mid, Bp, t, stream, blocksToRun);
         if (heads)
-            check(azh::launchHeads(x, weights.heads, s.dAct + (size_t)b0 * 3 * sh.A, s.dLogits + (size_t)b0 * sh.A1,
-                                   s.dValues + b0, s.dOwn ? s.dOwn + (size_t)b0 * sh.A : nullptr, Bp, sh.n, sh.F,
-                                   sh.V, stream),
+            check(azh::launchHeads(io.x, weights.heads, io.act, io.logits, io.values, io.own, Bp, sh.n, sh.F, sh.V,
+                                   stream),
                   "heads");
     }
 
@@ -1038,7 +1095,7 @@ struct azh_runner {
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
         const bool small = useSmallTower(B);
         overHalves(s, B, stream, [&](int b0, int Bp, hipStream_t st) {
-            launchPassPart(s, b0, Bp, partTiling(B, Bp), st, blocksToRun, heads, small);
+            launchPassPart(slotBuffers(s, b0), Bp, partTiling(B, Bp), st, blocksToRun, heads, small);
         });
     }
 
@@ -1211,6 +1268,8 @@ void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, i
     const azh_hub_group one{1, slots, max_batch};
     admitRunners(*cfg, &one, 1);
     std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
+    check(hipGetDevice(&r->device), "hipGetDevice");
+    scratchOnCurrentDevice();   // azh_infer_noalloc's scratch, resolved at set-up on the runner's device
     uploadWeights(*cfg, given, r->weights);
     r->initTowerLayout();
     for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));
@@ -1412,6 +1471,37 @@ int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* va
         check(hipStreamSynchronize(s.stream), "GPU inference failed");
         std::memcpy(logits, s.hLogits, (size_t)B * r->shape.A1 * sizeof(float));
         std::memcpy(values, s.hValues, (size_t)B * sizeof(float));
+    });
+}
+
+int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership,
+                      void* stream) {
+    return guarded([&] {
+        if (!r || !input || !logits || !values)
+            throw Error(AZH_ERR_ARGUMENT, "hip: infer_noalloc needs a runner and device input, logits and values");
+        if (ownership && !r->shape.ownership) throw Error(AZH_ERR_ARGUMENT, "hip: the network has no ownership head");
+        if (B < 1) throw Error(AZH_ERR_ARGUMENT, "hip: batch of " + std::to_string(B) + " positions");
+        const Shape& sh = r->shape;
+        const size_t need = noallocScratchFloats(sh, B) * sizeof(float);
+        if (need > kScratchBytes) {
+            int most = (int)(kScratchBytes / (need / B));
+            while (most > 0 && noallocScratchFloats(sh, most) * sizeof(float) > kScratchBytes) --most;
+            throw Error(AZH_ERR_ARGUMENT, "hip: a pass of " + std::to_string(B) + " positions needs " +
+                                              std::to_string(need) + " bytes of scratch; azh_infer_noalloc holds " +
+                                              std::to_string(kScratchBytes) + " (at most " + std::to_string(most) +
+                                              " positions of this network per call)");
+        }
+        int dev = 0;
+        check(hipGetDevice(&dev), "hipGetDevice");
+        if (dev != r->device)
+            throw Error(AZH_ERR_STATE, "hip: the runner lives on device " + std::to_string(r->device) + ", device " +
+                                           std::to_string(dev) + " is current");
+        float* x = scratchOnCurrentDevice();
+        float* mid = x + alignFloats(azh::quadFloats(B, sh.F, sh.A));
+        float* act = mid + alignFloats(azh::quadFloats(B, sh.F, sh.A));
+        r->launchPassPart(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B,
+                          azh::chooseConvTiling(sh.F, B, sh.n), static_cast<hipStream_t>(stream), sh.blocks, true,
+                          r->useSmallTower(B));
     });
 }
 

@@ -181,6 +181,25 @@ int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user);
  * CudaInference refuses it. */
 int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). azh_infer's pass on device arrays, enqueued on `stream`
+ * (a hipStream_t; NULL: the null stream) without waiting and without
+ * allocating: input [B][planes][area], logits [B][area+1], values [B] and,
+ * when not NULL, ownership [B][area] (the network must have the head) are
+ * the caller's device memory; the pass's own intermediates go to a static
+ * 96 MiB device array per GPU, held until the process ends (256 boards of a
+ * 19x19 network of 128 filters fit). A batch that needs more is
+ * AZH_ERR_ARGUMENT, naming the most positions one call takes. Every call on
+ * a GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race and must be ordered by the caller. Nothing in the
+ * array needs to start at zero (every element a pass reads is written
+ * earlier in the same pass). The runner's device must be current; no slot
+ * is used, so slots' passes may run meanwhile. Same kernels, same bits as
+ * azh_infer. */
+int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership,
+                      void* stream);
+
 /* The legal-move softmax on the GPU (no reference counterpart on the GPU; it
  * restates Mcts::expand's priors, src/mcts.cpp:170-183): priors[b][a] =
  * exp(l - max) / sum over legal of the same, 0 where legal[b][a] == 0.
