@@ -1,10 +1,12 @@
 // Drives the hip backend's C++ adapter (alphazero-go_amd/host/) through the
-// REFERENCE's own InferenceHub, Network and BatchRunner contract, compiled
-// from the reference's sources (oracle/Makefile, target hubdriver). The
-// scenarios follow the reference's runner and hub tests
-// (tests/test_cuda.cpp:1022-1237, tests/test_inference_hub.cpp:272-628).
+// REFERENCE's own InferenceHub, Network and BatchRunner contract, and through
+// its unchanged self-play and arena code, compiled from the reference's
+// sources with the `hip` name sites of oracle/hip_names.patch (oracle/Makefile,
+// target hubdriver). The scenarios follow the reference's runner, hub and
+// engine tests (tests/test_cuda.cpp:1022-1348, tests/test_inference_hub.cpp:272-628).
 //
 //   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain | ownership | throughput
+//                                         | names | selfplay | arena
 //
 // Prints "PASS <scenario>" and exits 0, or prints what failed and exits 1.
 #include <algorithm>
@@ -14,15 +16,21 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <thread>
 #include <vector>
 
+#include "azgo/arena.hpp"
 #include "azgo/backend.hpp"
+#include "azgo/config.hpp"
 #include "azgo/inference_hub.hpp"
 #include "azgo/network.hpp"
+#include "azgo/replay_buffer.hpp"
 #include "azgo/rng.hpp"
+#include "azgo/selfplay_slice.hpp"
+#include "azgo/serialize.hpp"
 #include "hip.hpp"
 
 using namespace azgo;
@@ -400,11 +408,180 @@ void throughput() {
     throughputOf(config(9, 6, 64, 64), 256, 3.0);
 }
 
+// The name sites (oracle/hip_names.patch) as the reference's callers meet
+// them: `hip` is available here, maps to blas for CPU work, is no
+// per-operation backend, is an engine and not a run's backend in a config,
+// and WorkerEvaluators(net, "hip", ...) gives every worker an evaluator on
+// one hub whose rows equal each position alone (test_worker_evaluators_cuda,
+// tests/test_cuda.cpp:1240-1258).
+void names() {
+    bool threw = false;
+    try {
+        checkBackendAvailable("hip");
+    } catch (const std::exception& e) {
+        std::printf("checkBackendAvailable(hip): %s\n", e.what());
+        threw = true;
+    }
+    expect(!threw, "checkBackendAvailable accepts hip on a gfx950 GPU");
+    expect(cpuBackendName("hip") == "blas", "hip's CPU work runs on blas");
+    std::string what;
+    try {
+        makeBackend("hip", 1);
+    } catch (const std::invalid_argument& e) {
+        what = e.what();
+    }
+    expect(what.find("not a per-operation backend") != std::string::npos, "makeBackend refuses hip: " + what);
+    what.clear();
+    try {
+        parseConfigText("backend = hip\n", "names.cfg");
+    } catch (const std::exception& e) {
+        what = e.what();
+    }
+    expect(what.find("hip is an engine only") != std::string::npos, "a run's backend = hip is refused: " + what);
+
+    const NetConfig cfg = config(9, 2, 16, 16);
+    const Network net = randomNetwork(cfg, 708);
+    const int workers = 8, per = 8, actions = cfg.actions();
+    const size_t planeFloats = static_cast<size_t>(cfg.planes()) * cfg.area();
+    Rng rng(709);
+    const std::vector<float> positions = randomPositions(cfg, workers * per, rng);
+    std::vector<float> aloneLogits(static_cast<size_t>(workers) * per * actions), aloneValues(workers * per);
+    {
+        HipInference gpu(net, 1);
+        for (int i = 0; i < workers * per; ++i)
+            gpu.infer(positions.data() + i * planeFloats, 1, aloneLogits.data() + static_cast<size_t>(i) * actions,
+                      aloneValues.data() + i);
+    }
+    WorkerEvaluators evaluators(net, "hip", workers, per, 256);
+    expect(evaluators.hub() != nullptr && evaluators.workers() == workers, "WorkerEvaluators builds one hip hub");
+    std::atomic<int> mismatches{0};
+    std::vector<std::thread> threads;
+    for (int w = 0; w < workers; ++w)
+        threads.emplace_back([&, w] {
+            std::vector<float> logits(static_cast<size_t>(per) * actions), values(per);
+            evaluators.forWorker(w).evaluate(positions.data() + w * per * planeFloats, per, logits.data(),
+                                             values.data());
+            if (!sameBits(logits.data(), aloneLogits.data() + static_cast<size_t>(w) * per * actions,
+                          static_cast<size_t>(per) * actions) ||
+                !sameBits(values.data(), aloneValues.data() + w * per, per))
+                ++mismatches;
+        });
+    for (std::thread& t : threads) t.join();
+    std::printf("names: %lld evaluations through WorkerEvaluators(hip), %d workers differ from alone\n",
+                evaluators.evaluations(), mismatches.load());
+    expect(mismatches.load() == 0, "every worker's rows equal its positions alone");
+    expect(evaluators.evaluations() == workers * per, "the hub counted every position");
+}
+
+// A slice's games as the bytes its result file carries: each GameRecord
+// serialized by writeGameRecord (include/azgo/replay_buffer.hpp:47).
+std::string gameBytes(const std::vector<GameRecord>& games) {
+    std::ostringstream out;
+    BinaryWriter w(out);
+    for (const GameRecord& g : games) writeGameRecord(w, g);
+    return out.str();
+}
+
+// The determinism contract of a GPU engine's self-play slice, through the
+// reference's unchanged playSelfPlayGames, MCTS and hub: the same games,
+// byte for byte, for 1, 3 and 8 workers, passes capped at 8 or 256
+// positions, and the hub's chaos mode off and on
+// (test_selfplay_slice_independent_of_workers_and_batching,
+// tests/test_cuda.cpp:1270-1298).
+void selfplay() {
+    for (const NetConfig& cfg : {config(5, 1, 8, 16), config(9, 2, 16, 16)}) {
+        const Network net = randomNetwork(cfg, 801);
+        SelfPlayConfig sp;
+        sp.mcts.simulations = 32;
+        sp.mcts.batchSize = 8;
+        sp.temperatureMoves = 6;
+        std::string first;
+        int runs = 0;
+        long long evaluations = 0;
+        for (int workers : {1, 3, 8})
+            for (int cap : {8, 256})
+                for (uint64_t chaos : {0ull, 21ull}) {
+                    hip_probe::setHubChaosSeed(chaos);
+                    EngineRun run;
+                    run.backend = "hip";
+                    run.workers = workers;
+                    run.inferenceBatch = cap;
+                    SliceStats stats;
+                    const std::string bytes = gameBytes(playSelfPlayGames(net, sp, 802, 3, 10, 6, run, &stats));
+                    hip_probe::setHubChaosSeed(0);
+                    expect(stats.evaluations > 0, "the slice evaluated positions on the GPU");
+                    evaluations += stats.evaluations;
+                    if (first.empty()) first = bytes;
+                    expect(bytes == first, "workers " + std::to_string(workers) + ", cap " + std::to_string(cap) +
+                                               ", chaos " + std::to_string(chaos) + ": the same game bytes");
+                    ++runs;
+                }
+        std::printf("selfplay %dx%d %dx%d: %d runs of 6 games, %zu bytes each, %lld positions evaluated\n",
+                    cfg.boardSize, cfg.boardSize, cfg.blocks, cfg.filters, runs, first.size(), evaluations);
+        std::fflush(stdout);
+    }
+}
+
+// An arena wave on the hip engine (one hub per network, several networks
+// sharing the GPU, every game at once), through the reference's unchanged
+// playArenaGames: the same games, move for move, for any workers, pass cap
+// and chaos, and slices of the wave joined play what the whole wave plays
+// (test_arena_wave_independent_of_workers_and_batching,
+// tests/test_cuda.cpp:1300-1348).
+void arena() {
+    const NetConfig cfg = config(5, 1, 8, 16);
+    const Network a = randomNetwork(cfg, 811), b = randomNetwork(cfg, 812), c = randomNetwork(cfg, 813);
+    ArenaConfig ac;
+    ac.simulations = 16;
+    ac.mctsBatch = 4;
+    ac.temperatureMoves = 2;
+    const std::vector<ArenaMatchSpec> wave = {
+        {ArenaPlayer::network(a), ArenaPlayer::network(b), 6, 901},
+        {ArenaPlayer::network(a), ArenaPlayer::bot(8), 4, 902},
+        {ArenaPlayer::network(a), ArenaPlayer::network(c), 4, 903},
+    };
+    auto played = [](const std::vector<ArenaGameResult>& games) {
+        std::string out;
+        for (const ArenaGameResult& g : games) {
+            out += std::to_string(g.scoreA) + ":";
+            for (int m : g.moves) out += std::to_string(m) + ",";
+            out += ";";
+        }
+        return out;
+    };
+    std::string whole;
+    int runs = 0;
+    for (int workers : {1, 3, 0})
+        for (int cap : {8, 256})
+            for (uint64_t chaos : {0ull, 23ull}) {
+                hip_probe::setHubChaosSeed(chaos);
+                EngineRun run;
+                run.backend = "hip";
+                run.workers = workers;
+                run.inferenceBatch = cap;
+                SliceStats stats;
+                const std::string games = played(playArenaGames(waveSlice(wave, 0, 14), ac, run, &stats));
+                hip_probe::setHubChaosSeed(0);
+                expect(stats.evaluations > 0, "the wave evaluated positions on the GPU");
+                if (whole.empty()) whole = games;
+                expect(games == whole, "workers " + std::to_string(workers) + ", cap " + std::to_string(cap) +
+                                           ", chaos " + std::to_string(chaos) + ": the same games");
+                ++runs;
+            }
+    EngineRun run;
+    run.backend = "hip";
+    const std::string joined = played(playArenaGames(waveSlice(wave, 0, 5), ac, run)) +
+                               played(playArenaGames(waveSlice(wave, 5, 9), ac, run));
+    expect(joined == whole, "slices [0, 5) and [5, 14) joined play the whole wave's games");
+    std::printf("arena: %d runs of a 14-game wave over 3 networks and a bot, %zu bytes of moves each\n", runs,
+                whole.size());
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
     if (argc != 2) {
-        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership|throughput\n");
+        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership|throughput|names|selfplay|arena\n");
         return 2;
     }
     std::string why;
@@ -421,6 +598,9 @@ int main(int argc, char** argv) {
         else if (s == "ownership") ownership();
         else if (s == "drain") drain();
         else if (s == "throughput") throughput();
+        else if (s == "names") names();
+        else if (s == "selfplay") selfplay();
+        else if (s == "arena") arena();
         else {
             std::printf("unknown scenario %s\n", s.c_str());
             return 2;
