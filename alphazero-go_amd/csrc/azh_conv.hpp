@@ -50,25 +50,31 @@ struct Geo {
 // input), so the compiler cannot move a residual read above an earlier
 // store: all of a lane's residual quads are read first, in one batch, then
 // combined and stored.
+//
+// What the epilogue reads besides the accumulators (a lane's BN factors and
+// residual quads) does not depend on the convolution, so the small-tile
+// body reads it before its first MFMA.
+template <int COW, int PPW>
+struct EpilogueInputs {
+    float sc[COW][4], sh[COW][4];
+    f4 res[COW][PPW];
+};
+
 template <int N, int COW, int PPW>
-__device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const float* __restrict__ scale,
-                                             const float* __restrict__ shift, const float* skip, float* y, int b,
-                                             int cout, int cb0, int pg0, int k, int n16, int relu) {
+__device__ __forceinline__ void loadEpilogue(EpilogueInputs<COW, PPW>& e, const float* __restrict__ scale,
+                                             const float* __restrict__ shift, const float* skip, int b, int cout,
+                                             int cb0, int pg0, int k, int n16) {
     using G = Geo<N>;
     const int quads = (cout + 3) / 4;
-    const size_t board = (size_t)b * quads * G::A;   // in float4 units
-    const f4* skipq = skip ? reinterpret_cast<const f4*>(skip) + board : nullptr;
-    f4* yq = reinterpret_cast<f4*>(y) + board;
-    float sc[COW][4], sh[COW][4];
+    const f4* skipq = skip ? reinterpret_cast<const f4*>(skip) + (size_t)b * quads * G::A : nullptr;
 #pragma unroll
     for (int c = 0; c < COW; ++c)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int co = min((cb0 + c) * 16 + 4 * k + r, cout - 1);
-            sc[c][r] = scale[co];
-            sh[c][r] = shift[co];
+            e.sc[c][r] = scale[co];
+            e.sh[c][r] = shift[co];
         }
-    f4 res[COW][PPW];
     if (skipq) {
 #pragma unroll
         for (int c = 0; c < COW; ++c)
@@ -78,9 +84,18 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
                 // values are never stored.
                 const int g = min((cb0 + c) * 4 + k, quads - 1);
                 const int p = min((pg0 + j) * 16 + n16, G::A - 1);
-                res[c][j] = skipq[(size_t)g * G::A + p];
+                e.res[c][j] = skipq[(size_t)g * G::A + p];
             }
     }
+}
+
+template <int N, int COW, int PPW>
+__device__ __forceinline__ void writeOutputs(const f4 (&acc)[COW][PPW], const EpilogueInputs<COW, PPW>& e,
+                                             bool addSkip, float* y, int b, int cout, int cb0, int pg0, int k,
+                                             int n16, int relu) {
+    using G = Geo<N>;
+    const int quads = (cout + 3) / 4;
+    f4* yq = reinterpret_cast<f4*>(y) + (size_t)b * quads * G::A;
 #pragma unroll
     for (int c = 0; c < COW; ++c) {
         const int g = (cb0 + c) * 4 + k;
@@ -91,12 +106,263 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
             f4 o;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                o[r] = 4 * g + r < cout ? epilogue(acc[c][j][r], sc[c][r], sh[c][r], skipq != nullptr, res[c][j][r],
+                o[r] = 4 * g + r < cout ? epilogue(acc[c][j][r], e.sc[c][r], e.sh[c][r], addSkip, e.res[c][j][r],
                                                    relu != 0)
                                         : 0.0f;
             if (p < G::A) yq[(size_t)g * G::A + p] = o;
         }
     }
+}
+
+template <int N, int COW, int PPW>
+__device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const float* __restrict__ scale,
+                                             const float* __restrict__ shift, const float* skip, float* y, int b,
+                                             int cout, int cb0, int pg0, int k, int n16, int relu) {
+    EpilogueInputs<COW, PPW> e;
+    loadEpilogue<N, COW, PPW>(e, scale, shift, skip, b, cout, cb0, pg0, k, n16);
+    writeOutputs<N, COW, PPW>(acc, e, skip != nullptr, y, b, cout, cb0, pg0, k, n16, relu);
+}
+
+// The small pixel tiles (the shapes of small batches): a workgroup of WPG
+// waves owns one board, one block of 16 output channels and WPG x PPW of its
+// 16-point column groups, PPW per wave. A tap there is only 4 x PPW MFMAs,
+// far shorter than a global load's round trip, so:
+//  - everything chunk q needs (its board planes, staged as the general body
+//    stages them, and its nine taps' A fragments for the block of 16
+//    channels, fetched once per workgroup instead of once per wave) is
+//    loaded into registers during chunk q - 2 and stored into LDS during
+//    chunk q - 1, whose barrier publishes it;
+//  - the loads and stores are spread over the taps of the MFMA stream, one
+//    item per tap, on addresses computed once (a chunk adds only a uniform
+//    offset), so their few instructions issue between the MFMAs instead of
+//    holding them up;
+//  - the loads are unconditional (an item past the tile loads a valid
+//    element and stores to a spare LDS cell; channels past cin are zeroed
+//    at the store): loads under a branch would leave the compiler's count
+//    of loads in flight unsure at the merge, and it would wait for all;
+//  - the load registers alternate between two sets with the chunks, and the
+//    chunk loop runs in pairs so that each set is fixed at compile time: no
+//    register copy waits on a load in flight;
+//  - the LDS tile holds only the board rows the workgroup's points touch,
+//    with a zero row above and below (the whole haloed board on the wider
+//    tiles);
+//  - a tap's A fragment is read from LDS one tap ahead, the B operands in
+//    the general body's ring;
+//  - the epilogue's BN factors and residual quads are read before the first
+//    MFMA (they do not depend on this convolution).
+// The MFMA sequence per output (chunk, tap, channel in chunk) and every
+// operand are the general body's, so the bits are too.
+template <int N, int WPG, int PPW, bool PLANAR>
+__device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, const f4* __restrict__ wp,
+                                                 const float* __restrict__ scale, const float* __restrict__ shift,
+                                                 const float* skip, float* y, int cin, int cout, int nq, int coTiles,
+                                                 int pixTiles, int relu) {
+    using G = Geo<N>;
+    constexpr int THREADS = WPG * 64;
+    constexpr int SPAN = WPG * PPW * 16;
+    constexpr int ROWS = (SPAN - 1) / N + 4 < N ? (SPAN - 1) / N + 4 : N;   // staged rows, at most
+    constexpr int GC = (ROWS + 2) * G::H;     // one channel group's tile: staged rows and two zero rows
+    constexpr int CB = 4 * GC;                // one chunk's tile (float4 cells)
+    constexpr int ITEMS = 4 * ROWS * N;       // (channel group, point) pairs per chunk, at most
+    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
+    constexpr int AITEMS = 9 * 64;            // one block's A fragments per chunk (float4 units)
+    constexpr int APER = (AITEMS + THREADS - 1) / THREADS;
+    constexpr int NI = PER + APER;            // a thread's items per chunk
+    // Two chunk buffers of board planes and of A fragments, and a spare cell
+    // each for stores of items past the tile.
+    __shared__ f4 lds[2 * CB + 1];
+    __shared__ f4 alds[2 * AITEMS + 1];
+    constexpr int kSpare = 2 * CB, kSpareA = 2 * AITEMS;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Co tiles of one board on one XCD (as the general body numbers them).
+    const int total = gridDim.x;
+    const int wg = blockIdx.x;
+    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
+    const int tilesPerBoard = coTiles * pixTiles;
+    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
+    const int cb0 = tile / pixTiles, pt = tile % pixTiles;
+    const int pg0 = (pt * WPG + wave) * PPW;
+    const int k = lane >> 4, n16 = lane & 15;
+
+    for (int i = tid; i < 2 * CB; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // The staged rows [rowLo, rowLo + span / N): the tile's points' rows and
+    // one more on each side, clamped to the board. Tile row r - rowLo + 1
+    // holds board row r; the rows above and below stay zero, and are read
+    // only where they are off the board.
+    int rowLo = 0, span = G::A;
+    if (SPAN < G::A) {
+        const int p0 = pt * SPAN;
+        const int p1 = min(G::A, p0 + SPAN);
+        rowLo = max(0, p0 / N - 1);
+        span = (min(N - 1, (p1 - 1) / N + 1) - rowLo + 1) * N;
+    }
+    const int items = 4 * span, first = rowLo * N;
+    int rofs[PPW];   // a lane's B read position per column group (float4 cells; taps added as constants)
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) {
+        int p = (pg0 + j) * 16 + n16;
+        p = p < G::A ? p : G::A - 1;   // points past the board read a valid cell; never stored
+        rofs[j] = k * GC + (p / N - rowLo) * G::H + (p % N);
+    }
+
+    // Per item, computed once: where it loads from (relative to a chunk's
+    // first plane or quad, and in the last chunk, where quads past cin
+    // fall back to the last quad), which LDS cell of each buffer it goes to,
+    // and whether the last chunk zeroes it.
+    const int lastQuad = (cin - 1) / 4;
+    const int qLast = nq - 1;
+    const float* xb = x + (size_t)b * cin * G::A;                                        // PLANAR
+    const f4* xq = reinterpret_cast<const f4*>(x) + (size_t)b * ((cin + 3) / 4) * G::A;   // channel quads
+    const f4* wb = wp + (size_t)cb0 * nq * AITEMS;   // this block's fragments, [chunk][tap][lane]
+    int pOff[PER], pOffLast[PER], pG[PER], pCell0[PER], pCell1[PER];
+    bool pZeroLast[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int it = tid + r * THREADS;
+        const int itc = min(it, items - 1);
+        const int g = itc / span, p = first + itc - g * span;
+        pG[r] = g;
+        const int gLast = min(g, lastQuad - 4 * qLast);   // >= 0: chunk qLast holds at least one quad
+        pOff[r] = PLANAR ? 4 * g * G::A + p : g * G::A + p;
+        pOffLast[r] = gLast * G::A + p;
+        pZeroLast[r] = 4 * qLast + g > lastQuad;
+        const int cell = g * GC + (p / N - rowLo + 1) * G::H + (p % N + 1);
+        pCell0[r] = it < items ? cell : kSpare;
+        pCell1[r] = it < items ? CB + cell : kSpare;
+    }
+    int aSrc[APER], aCell0[APER], aCell1[APER];
+#pragma unroll
+    for (int r = 0; r < APER; ++r) {
+        const int it = tid + r * THREADS;
+        const bool in = AITEMS % THREADS == 0 || it < AITEMS;
+        aSrc[r] = min(it, AITEMS - 1);
+        aCell0[r] = in ? it : kSpareA;
+        aCell1[r] = in ? AITEMS + it : kSpareA;
+    }
+    // Item i (planes first, then fragments) of chunk q into a register set,
+    // and from it into LDS buffer `buf`.
+    auto loadItem = [&](int i, int q, f4 (&sp)[PER], f4 (&sa)[APER]) {
+        if (i < PER) {
+            const int r = i;
+            if (PLANAR) {
+                // plane q*16 + 4g + c at xb + plane * A + p
+                const int c0 = q * 16 + 4 * pG[r];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int ch = min(c0 + c, cin - 1);
+                    sp[r][c] = xb[pOff[r] + (ch - 4 * pG[r]) * G::A];
+                }
+            } else {
+                sp[r] = (xq + (size_t)q * 4 * G::A)[q == qLast ? pOffLast[r] : pOff[r]];
+            }
+        } else {
+            const int r = i - PER;
+            sa[r] = (wb + (size_t)q * AITEMS)[aSrc[r]];
+        }
+    };
+    auto storeItem = [&](int i, int buf, int q, const f4 (&sp)[PER], const f4 (&sa)[APER]) {
+        if (i < PER) {
+            const int r = i;
+            f4 v = sp[r];
+            if (PLANAR) {
+                const int c0 = q * 16 + 4 * pG[r];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = c0 + c < cin ? v[c] : 0.0f;
+            } else {
+                // a quad past cin is zeros (a quad's own channels past cin are stored zeros)
+                v = q == qLast && pZeroLast[r] ? f4{0.0f, 0.0f, 0.0f, 0.0f} : v;
+            }
+            lds[buf ? pCell1[r] : pCell0[r]] = v;
+        } else {
+            const int r = i - PER;
+            alds[buf ? aCell1[r] : aCell0[r]] = sa[r];
+        }
+    };
+
+    // The epilogue's inputs, unconditionally (without a residual, the
+    // output's own quads are read and ignored).
+    EpilogueInputs<1, PPW> ep;
+    loadEpilogue<N, 1, PPW>(ep, scale, shift, skip ? skip : y, b, cout, cb0, pg0, k, n16);
+
+    f4 acc[1][PPW];
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) acc[0][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Chunks 0 and 1 in flight; chunk 0 published. A chunk past the last is
+    // loaded as the last one again, stored into a buffer nobody reads
+    // afterwards, and not multiplied.
+    f4 p0[PER], a0[APER], p1[PER], a1[APER];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) loadItem(i, 0, p0, a0);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) loadItem(i, min(1, qLast), p1, a1);
+    __syncthreads();   // the zero fill is complete before any interior store
+#pragma unroll
+    for (int i = 0; i < NI; ++i) storeItem(i, 0, 0, p0, a0);
+    __syncthreads();
+
+    constexpr int kRing = 4;
+    constexpr int STEPS = 9 * PPW;
+    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
+    // Chunk q from LDS buffer `buf` (q & 1): tap t loads items [t*NI/9,
+    // (t+1)*NI/9) of chunk q + 2 into the free register set (pNew, aNew) and
+    // stores the same items of chunk q + 1 (pNext, aNext: loaded during
+    // chunk q - 1) into the other buffer, free since the barrier that ended
+    // chunk q - 1. The last chunk stores a copy of itself there, never read.
+    auto chunk = [&](int q, int buf, f4 (&pNew)[PER], f4 (&aNew)[APER], const f4 (&pNext)[PER],
+                     const f4 (&aNext)[APER]) {
+        const int qn = min(q + 2, qLast), qs = min(q + 1, qLast);
+        const f4* bb = lds + buf * CB;
+        const f4* ab = alds + buf * AITEMS + lane;
+        f4 ring[kRing];
+#pragma unroll
+        for (int i = 0; i < kRing && i < STEPS; ++i) ring[i] = bb[rofs[i % PPW] + tapOffset(i / PPW)];
+        f4 aT[2];
+        aT[0] = ab[0];
+        __builtin_amdgcn_sched_group_barrier(0x100, kRing + 1, 0);   // the ring's first reads, tap 0's fragment
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+            const int t = i / PPW, pg = i % PPW;
+            if (pg == 0) {
+                const int i0 = t * NI / 9, i1 = (t + 1) * NI / 9;
+#pragma unroll
+                for (int it = i0; it < i1; ++it) {
+                    loadItem(it, qn, pNew, aNew);
+                    if (it < PER)
+                        __builtin_amdgcn_sched_group_barrier(0x020, PLANAR ? 4 : 1, 0);
+                    else
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+#pragma unroll
+                for (int it = i0; it < i1; ++it) {
+                    storeItem(it, buf ^ 1, qs, pNext, aNext);
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                }
+                if (t + 1 < 9) {
+                    aT[(t + 1) & 1] = ab[(t + 1) * 64];   // the next tap's fragment, a tap ahead
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+            const f4 bv = ring[i % kRing];
+            if (i + kRing < STEPS) ring[i % kRing] = bb[rofs[(i + kRing) % PPW] + tapOffset((i + kRing) / PPW)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[0][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[t & 1][j], bv[j], acc[0][pg], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                         // step i's MFMAs,
+            if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
+        }
+        __syncthreads();
+    };
+    int q = 0;
+    for (; q + 1 < nq; q += 2) {
+        chunk(q, 0, p0, a0, p1, a1);
+        chunk(q + 1, 1, p1, a1, p0, a0);
+    }
+    if (q < nq) chunk(q, 0, p0, a0, p1, a1);
+
+    writeOutputs<N, 1, PPW>(acc, ep, skip != nullptr, y, b, cout, cb0, pg0, k, n16, relu);
 }
 
 // A workgroup computes one board's output channels [co tile] at column
@@ -122,12 +388,6 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     constexpr int ROWS = PPW0 == 0 ? N : ((SPAN - 1) / N + 4 < N ? (SPAN - 1) / N + 4 : N);
     constexpr int ITEMS = 4 * ROWS * N;   // (channel group, point) pairs per chunk, at most
     constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
-    // Small pixel tiles on the larger boards (the small batches' shapes at
-    // 13x13 and 19x19): a tap is only 4 x PPW MFMAs there, far shorter than
-    // a global load's round trip, so the A fragments are fetched a whole
-    // chunk ahead (the nine taps of chunk q+1 during chunk q) instead of one
-    // tap ahead, and the board planes two chunks ahead instead of one.
-    constexpr bool SMALL = PPW0 != 0 && PPW0 <= 2 && N >= 13;
     __shared__ f4 lds[2 * G::BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -171,7 +431,7 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
 
     const float* xb = x + (size_t)b * cin * G::A;                                  // PLANAR
     const f4* xq = reinterpret_cast<const f4*>(x) + (size_t)b * ((cin + 3) / 4) * G::A;   // channel quads
-    f4 stage[PER], stage2[SMALL ? PER : 1];
+    f4 stage[PER];
     auto load = [&](int q, f4* dst) {
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
@@ -212,9 +472,6 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     load(0, stage);
     __syncthreads();   // the zero fill is complete before any interior store
     store(0);
-    // Two chunks ahead: chunk 1 waits in `stage` while chunk 0 is multiplied
-    // (with one chunk, chunk 0 again, never stored).
-    if (SMALL) load(min(1, nq - 1), stage);
     __syncthreads();
 
     // The (tap, column group) steps of a chunk run as one unrolled stream:
@@ -233,19 +490,12 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
     };
     f4 aCur[COW], aNext[COW];
-    f4 aChunk[SMALL ? 9 : 1][COW], aChunkNext[SMALL ? 9 : 1][COW];
-    if (SMALL) {
-#pragma unroll
-        for (int t = 0; t < 9; ++t) loadA(0, t, aChunk[t]);
-    } else {
-        loadA(0, 0, aCur);
-    }
+    loadA(0, 0, aCur);
     for (int q = 0; q < nq; ++q) {
-        // The last chunks fetch the last one again in place of chunks that
-        // do not exist (never stored), which keeps the step stream free of
+        // The last chunk fetches itself again in place of a chunk that does
+        // not exist (never stored), which keeps the step stream free of
         // branches.
         const int qn = q + 1 < nq ? q + 1 : q;
-        const int q2 = q + 2 < nq ? q + 2 : nq - 1;
         const f4* buf = lds + (q & 1) * G::BUF;
         f4 ring[kRing];
 #pragma unroll
@@ -255,23 +505,14 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         for (int i = 0; i < STEPS; ++i) {
             const int t = i / PPW, pg = i % PPW;
             if (pg == 0) {
-                // The next tap's A fragments (tap 8: the next chunk's first;
-                // SMALL: this tap's of the next chunk), and at tap 0 after
-                // them the board planes of the next chunk (SMALL: the one
-                // after it; the next waits in `stage`): the count of
-                // outstanding loads drains in issue order, so a tap's wait
-                // for its fragments does not wait for the planes.
-                if (SMALL)
-                    loadA(qn, t, aChunkNext[t]);
-                else
-                    loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
+                // The next tap's A fragments (tap 8: the next chunk's first),
+                // and at tap 0 after them the board planes of the next
+                // chunk: the count of outstanding loads drains in issue
+                // order, so a tap's wait for its fragments does not wait
+                // for the planes.
+                loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
                 __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);   // issued here, a tap ahead
-                if (t == 0) {
-                    if (SMALL)
-                        load(q2, stage2);
-                    else
-                        load(qn, stage);
-                }
+                if (t == 0) load(qn, stage);
             }
             const f4 bv = ring[i % kRing];
             if (i + kRing < STEPS)
@@ -280,26 +521,15 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int c = 0; c < COW; ++c)
-                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(SMALL ? aChunk[t][c][j] : aCur[c][j], bv[j],
-                                                                      acc[c][pg], 0, 0, 0);
+                    acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);                   // step i's MFMAs,
             if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then step i+kRing's read
-            if (!SMALL && pg == PPW - 1) {
+            if (pg == PPW - 1) {
 #pragma unroll
                 for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
             }
         }
-        if (SMALL) {
-#pragma unroll
-            for (int t = 0; t < 9; ++t)
-#pragma unroll
-                for (int c = 0; c < COW; ++c) aChunk[t][c] = aChunkNext[t][c];
-        }
         if (q + 1 < nq) store((q + 1) & 1);
-        if (SMALL) {
-#pragma unroll
-            for (int r = 0; r < PER; ++r) stage[r] = stage2[r];
-        }
         __syncthreads();
     }
 
@@ -318,8 +548,12 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         NAME(const float* __restrict__ x, const f4* __restrict__ wp, const float* __restrict__ scale,      \
              const float* __restrict__ shift, const float* skip, float* y, int cin, int cout, int nq,      \
              int coTiles, int pixTiles, int relu) {                                                        \
-        conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,   \
-                                                   pixTiles, relu);                                        \
+        if constexpr (PPW != 0 && COW * WCO == 1)                                                           \
+            conv3x3SmallBody<N, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,      \
+                                                  pixTiles, relu);                                         \
+        else                                                                                               \
+            conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, \
+                                                       pixTiles, relu);                                    \
     }
 AZH_CONV_KERNEL(conv3x3Tower, false)
 AZH_CONV_KERNEL(conv3x3Stem, true)

@@ -43,8 +43,8 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
 // and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
-// one point per thread, the trunk read in channel quads (sixteen 16-byte
-// loads per 64 channels) ahead of their FMAs:
+// one point per thread, the trunk read in channel quads (32 16-byte loads
+// per 128 channels) ahead of their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
 // src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
 // ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
@@ -54,30 +54,59 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
                                                                           HeadWeights w, float* __restrict__ act,
                                                                           float* __restrict__ own, int F) {
     constexpr int A = N * N;
+    constexpr int kRound = 128;   // channels per round
+    // A round's weights, channel by channel (policy 0, policy 1, value,
+    // ownership), staged in LDS and read by every thread at once as one
+    // 16-byte broadcast per channel. Channels past F, and the ownership row
+    // of a network without one, stage as zeros and their trunk values as
+    // zeros: fmaf(0, 0, a) is a for every accumulator a these sums reach
+    // (they start at +0 and never become -0), so the straight-line loop
+    // rounds exactly as the sum over channels 0..F-1 does.
+    __shared__ f4 wsh[kRound];
     const int b = blockIdx.x, p = threadIdx.x;
-    if (p >= A) return;
     const bool withOwn = own != nullptr;
     const int quads = (F + 3) / 4;
-    const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + p;
+    const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + min(p, A - 1);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    for (int c0 = 0; c0 < F; c0 += 64) {
-        float xv[64];
+    // 128 channels (32 quads) per round: a 128-filter trunk in one load
+    // round trip.
+    for (int c0 = 0; c0 < F; c0 += kRound) {
+        float xv[kRound];
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
+        for (int g = 0; g < kRound / 4; ++g) {
             const f4 v = c0 / 4 + g < quads ? tq[(size_t)(c0 / 4 + g) * A] : f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) xv[4 * g + r] = v[r];
+            for (int r = 0; r < 4; ++r) xv[4 * g + r] = c0 + 4 * g + r < F ? v[r] : 0.0f;
         }
+        __syncthreads();   // the previous round's weights are no longer read
+        for (int c = threadIdx.x; c < kRound; c += blockDim.x) {
+            const bool live = c0 + c < F;
+            f4 wv;
+            wv[0] = live ? w.convW[c0 + c] : 0.0f;
+            wv[1] = live ? w.convW[F + c0 + c] : 0.0f;
+            wv[2] = live ? w.convW[2 * F + c0 + c] : 0.0f;
+            wv[3] = live && withOwn ? w.convW[3 * F + c0 + c] : 0.0f;
+            wsh[c] = wv;
+        }
+        __syncthreads();
+        // Eight broadcasts in flight, then their 32 FMAs.
 #pragma unroll
-        for (int u = 0; u < 64; ++u) {
-            if (c0 + u < F) {
-                a0 = fmaf(w.convW[c0 + u], xv[u], a0);
-                a1 = fmaf(w.convW[F + c0 + u], xv[u], a1);
-                a2 = fmaf(w.convW[2 * F + c0 + u], xv[u], a2);
-                if (withOwn) a3 = fmaf(w.convW[3 * F + c0 + u], xv[u], a3);
+        for (int u0 = 0; u0 < kRound; u0 += 8) {
+            f4 wv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wv[j] = wsh[u0 + j];
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                a0 = fmaf(wv[j][0], xv[u0 + j], a0);
+                a1 = fmaf(wv[j][1], xv[u0 + j], a1);
+                a2 = fmaf(wv[j][2], xv[u0 + j], a2);
+                a3 = fmaf(wv[j][3], xv[u0 + j], a3);
             }
+            __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
         }
     }
+    if (p >= A) return;
     float* ab = act + (size_t)b * 3 * A;
     ab[p] = epilogue(a0, w.scale[0], w.shift[0], false, 0.0f, true);
     ab[A + p] = epilogue(a1, w.scale[1], w.shift[1], false, 0.0f, true);
@@ -116,27 +145,25 @@ __global__ __launch_bounds__(256) void headFcKernel(const float* __restrict__ ac
     const bool policy = (int)blockIdx.y < policyTiles;
     const int K = policy ? 2 * A : A, KPad = policy ? KP : KV;
     const int src = policy ? 0 : 2 * A;
-    // Stage the rows, eight loads in flight per thread: every load reads a
-    // valid element (act[0] in place of padding), and padding stores zero.
-    constexpr int kStage = 8;
-    const int total = kFcBoards * KPad;
-    for (int i0 = 0; i0 < total; i0 += 256 * kStage) {
-        float v[kStage];
-        bool ok[kStage];
+    // Stage the positions' rows: thread t holds columns t, t + 256, ... of
+    // every row, all of its loads in flight at once (one round trip); K
+    // padding and the rows past the batch are zeros, written without loads.
+    constexpr int KCOLS = (KP + 255) / 256;   // columns per thread (KP >= KV)
+    float v[kFcBoards][KCOLS];
 #pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = i0 + u * 256 + tid;
-            const int bb = i / KPad, k = i - bb * KPad;
-            ok[u] = i < total && bb < nb && k < K;
-            v[u] = act[ok[u] ? (size_t)(b0 + bb) * 3 * A + src + k : 0];
+    for (int bb = 0; bb < kFcBoards; ++bb)
+#pragma unroll
+        for (int c = 0; c < KCOLS; ++c) {
+            const int k = tid + 256 * c;
+            v[bb][c] = bb < nb && k < K ? act[(size_t)(b0 + bb) * 3 * A + src + k] : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = i0 + u * 256 + tid;
-            const int bb = i / KPad, k = i - bb * KPad;
-            if (i < total) xs[bb * RS + k] = ok[u] ? v[u] : 0.0f;
+    for (int bb = 0; bb < kFcBoards; ++bb)
+#pragma unroll
+        for (int c = 0; c < KCOLS; ++c) {
+            const int k = tid + 256 * c;
+            if (k < KPad) xs[bb * RS + k] = v[bb][c];
         }
-    }
     __syncthreads();
 
     const int m = lane & 15, kk = lane >> 4;

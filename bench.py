@@ -175,9 +175,9 @@ def stem_heads(workload, B, iters):
         trunk = rng.uniform(0, 2, (B, F, n * n)).astype(np.float32)
         for _ in range(iters):
             r.probe_heads(trunk)
-    ms = azgo_hip.time_conv3x3(B, n, cfg.planes, F, -1, iters)
+    ms = azgo_hip.time_conv3x3(B, n, cfg.planes, F, -1, iters)   # average per launch
     print(json.dumps({"mode": "stem-heads", "workload": f"{n}x{n} {blocks}x{F} batch {B}", "head_launches": iters,
-                      "stem_us_per_launch": round(ms / iters * 1e3, 2)}), flush=True)
+                      "stem_us_per_launch": round(ms * 1e3, 2)}), flush=True)
 
 
 def positions_leg(r, w, B, seen_per_position, iters=20):
