@@ -21,7 +21,7 @@ SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip", "azh_small
 # workgroup shape): azh_conv_inst.hip is compiled once per pair, so the
 # fully unrolled kernels build in parallel.
 CONV_INST = "azh_conv_inst.hip"
-CONV_HEADERS = ["azh_conv.hpp", "azh_conv_iface.hpp"]
+CONV_HEADERS = ["azh_conv.hpp", "azh_conv_iface.hpp", "azh_stem.hpp"]
 BOARD_SIZES = (5, 9, 13, 19)   # conv3x3Supported
 HEADERS = CONV_HEADERS + ["azh_kernels.hpp", "azh_heads.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
 

@@ -22,6 +22,7 @@
 // accumulator element r.
 #pragma once
 #include "azh_conv_iface.hpp"
+#include "azh_stem.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -355,12 +356,23 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
         }
         __syncthreads();
     };
+    // The stem's last chunk, unless cin fills it, is multiplied apart
+    // (stemTail), after the loop.
+    const bool tail = PLANAR && cin % kChunk != 0;
+    const int nqQuads = tail ? nq - 1 : nq;
     int q = 0;
-    for (; q + 1 < nq; q += 2) {
+    for (; q + 1 < nqQuads; q += 2) {
         chunk(q, 0, p0, a0, p1, a1);
         chunk(q + 1, 1, p1, a1, p0, a0);
     }
-    if (q < nq) chunk(q, 0, p0, a0, p1, a1);
+    if (q < nqQuads) chunk(q, 0, p0, a0, p1, a1);
+    if (tail) {
+        const int ql = nq - 1, buf = ql & 1;
+        // rofs[j] - k * GC is the lane's top-left cell.
+        stemTail<1, PPW, GC, G::H>(acc, reinterpret_cast<const float*>(alds + buf * AITEMS) + n16 * 4, 0,
+                                   reinterpret_cast<const float*>(lds + buf * CB - k * GC), rofs, k,
+                                   cin - ql * kChunk);
+    }
 
     writeOutputs<N, 1, PPW>(acc, ep, skip != nullptr, y, b, cout, cb0, pg0, k, n16, relu);
 }
@@ -372,7 +384,7 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
 // otherwise x is a trunk activation in channel quads, read a quad at a time.
 // Either way input channels past cin are read as zeros.
 template <int N, int COW, int WCO, int WPG, int PPW0, bool PLANAR>
-__device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f4* __restrict__ wp,
+__device__ __forceinline__ void conv3x3Body(f4* lds, const float* __restrict__ x, const f4* __restrict__ wp,
                                             const float* __restrict__ scale, const float* __restrict__ shift,
                                             const float* skip, float* y, int cin, int cout, int nq, int coTiles,
                                             int pixTiles, int relu) {
@@ -388,7 +400,6 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     constexpr int ROWS = PPW0 == 0 ? N : ((SPAN - 1) / N + 4 < N ? (SPAN - 1) / N + 4 : N);
     constexpr int ITEMS = 4 * ROWS * N;   // (channel group, point) pairs per chunk, at most
     constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
-    __shared__ f4 lds[2 * G::BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
@@ -491,7 +502,11 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
     };
     f4 aCur[COW], aNext[COW];
     loadA(0, 0, aCur);
-    for (int q = 0; q < nq; ++q) {
+    // The stem's last chunk, unless cin fills it, is multiplied apart
+    // (stemTail), after the loop.
+    const bool tail = PLANAR && cin % kChunk != 0;
+    const int nqQuads = tail ? nq - 1 : nq;
+    for (int q = 0; q < nqQuads; ++q) {
         // The last chunk fetches itself again in place of a chunk that does
         // not exist (never stored), which keeps the step stream free of
         // branches.
@@ -532,8 +547,160 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         if (q + 1 < nq) store((q + 1) & 1);
         __syncthreads();
     }
+    if (tail) {
+        const int q = nq - 1;
+        const float* wl =
+            reinterpret_cast<const float*>(wp) + (size_t)cb0 * nq * 9 * 256 + (size_t)q * 9 * 256 + n16 * 4;
+        // rofs[j] - k * HA is the lane's top-left cell.
+        stemTail<COW, PPW, G::HA, G::H>(acc, wl, (size_t)nq * 9 * 256,
+                                        reinterpret_cast<const float*>(lds + (q & 1) * G::BUF - k * G::HA), rofs,
+                                        k, cin - q * kChunk);
+    }
 
     storeOutputs<N, COW, PPW>(acc, scale, shift, skip, y, b, cout, cb0, pg0, k, n16, relu);
+}
+
+// The stem on whole boards (the shapes of large batches) when its planes
+// fit two chunks (cin <= 32: the network's 2H + 2 planes up to H = 15) and
+// nothing is added to its outputs (the network's stem adds nothing).
+// Both chunks are staged once; then each wave runs its column groups in two
+// halves, every K step of a half before its outputs are stored, so the
+// first half's stores drain while the second half multiplies (one pass over
+// the board would store everything after its last MFMA, with the matrix
+// units idle meanwhile), and the stem's last-chunk weights and BN factors
+// are fetched before the first MFMA (half the accumulators leave the
+// registers for them). The MFMA sequence per output, and so every bit, is
+// the general body's. lds: two chunk buffers of the general body's layout.
+template <int N, int COW, int WCO>
+__device__ __forceinline__ void conv3x3StemWhole(f4* lds, const float* __restrict__ x, const f4* __restrict__ wp,
+                                                 const float* __restrict__ scale, const float* __restrict__ shift,
+                                                 float* y, int cin, int cout, int nq, int coTiles, int relu) {
+    using G = Geo<N>;
+    constexpr int THREADS = WCO * 64;
+    constexpr int HALF = (G::NPG + 1) / 2;   // column groups per half (the second may hold one fewer)
+    constexpr int ITEMS = 4 * G::A;          // (channel group, point) pairs per chunk
+    constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Co tiles of one board on one XCD (as the general body numbers them).
+    const int total = gridDim.x;
+    const int wg = blockIdx.x;
+    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
+    const int b = logical / coTiles, ct = logical % coTiles;
+    const int cb0 = (ct * WCO + wave) * COW;
+    const int k = lane >> 4, n16 = lane & 15;
+
+    for (int i = tid; i < 2 * G::BUF; i += THREADS) lds[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Chunk q's planes into buffer q (planes past cin as zeros).
+    const float* xb = x + (size_t)b * cin * G::A;
+    auto load = [&](int q, f4 (&dst)[PER]) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                const int c0 = q * 16 + 4 * g;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (c0 + c < cin) v[c] = xb[(size_t)(c0 + c) * G::A + p];
+            }
+            dst[r] = v;
+        }
+    };
+    auto store = [&](int q, const f4 (&src)[PER]) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int it = tid + r * THREADS;
+            if (it < ITEMS) {
+                const int g = it / G::A, p = it - g * G::A;
+                lds[q * G::BUF + g * G::HA + (p / N + 1) * G::H + (p % N + 1)] = src[r];
+            }
+        }
+    };
+    {
+        f4 s0[PER], s1[PER];
+        load(0, s0);
+        load(1, s1);   // nq == 1: zeros, never read
+        __syncthreads();   // the zero fill is complete before any interior store
+        store(0, s0);
+        store(1, s1);
+    }
+    __syncthreads();
+
+    const bool tail = cin % kChunk != 0;
+    const int nqQuads = tail ? nq - 1 : nq;
+    const int qt = nq - 1;
+    const float* wl = reinterpret_cast<const float*>(wp) + ((size_t)cb0 * nq + qt) * 9 * 256 + n16 * 4;
+    const size_t blockStride = (size_t)nq * 9 * 256;
+    StemTail<COW, G::HA, G::H> st;
+    if (tail) st.fetch(wl, blockStride, k, cin - qt * kChunk);
+    EpilogueInputs<COW, HALF> ep;
+    loadEpilogue<N, COW, HALF>(ep, scale, shift, nullptr, b, cout, cb0, 0, k, n16);
+
+    constexpr int kRing = 4;
+    constexpr int STEPS = 9 * HALF;
+    auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
+    auto loadA = [&](int q, int t, f4 (&a)[COW]) {
+#pragma unroll
+        for (int c = 0; c < COW; ++c) a[c] = wp[((size_t)((cb0 + c) * nq + q) * 9 + t) * 64 + lane];
+    };
+    // The stream's A fragments, a tap ahead across chunks and halves.
+    f4 aCur[COW], aNext[COW];
+    loadA(0, 0, aCur);
+    for (int h = 0; h < 2; ++h) {
+        const int pg0 = h * HALF;
+        int rofs[HALF];
+#pragma unroll
+        for (int j = 0; j < HALF; ++j) {
+            int p = (pg0 + j) * 16 + n16;
+            p = p < G::A ? p : G::A - 1;   // points past the board read a valid cell; never stored
+            rofs[j] = k * G::HA + (p / N) * G::H + (p % N);
+        }
+        f4 acc[COW][HALF];
+#pragma unroll
+        for (int c = 0; c < COW; ++c)
+#pragma unroll
+            for (int j = 0; j < HALF; ++j) acc[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        // The general body's step stream per quad chunk (B operands kRing
+        // steps ahead, A fragments a tap ahead).
+        for (int q = 0; q < nqQuads; ++q) {
+            const f4* buf = lds + q * G::BUF;
+            const int qn = q + 1 < nqQuads ? q + 1 : 0;   // whose tap 0 follows tap 8
+            f4 ring[kRing];
+#pragma unroll
+            for (int i = 0; i < kRing; ++i) ring[i] = buf[rofs[i % HALF] + tapOffset(i / HALF)];
+            __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);
+#pragma unroll
+            for (int i = 0; i < STEPS; ++i) {
+                const int t = i / HALF, pg = i % HALF;
+                if (pg == 0) {
+                    loadA(t + 1 < 9 ? q : qn, (t + 1) % 9, aNext);
+                    __builtin_amdgcn_sched_group_barrier(0x020, COW, 0);
+                }
+                const f4 bv = ring[i % kRing];
+                if (i + kRing < STEPS)
+                    ring[i % kRing] = buf[rofs[(i + kRing) % HALF] + tapOffset((i + kRing) / HALF)];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int c = 0; c < COW; ++c)
+                        acc[c][pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(aCur[c][j], bv[j], acc[c][pg], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4 * COW, 0);
+                if (i + kRing < STEPS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (pg == HALF - 1) {
+#pragma unroll
+                    for (int c = 0; c < COW; ++c) aCur[c] = aNext[c];
+                }
+            }
+        }
+        // rofs[j] - k * HA is the lane's top-left cell.
+        if (tail)
+            st.multiply(acc, wl, blockStride, reinterpret_cast<const float*>(lds + qt * G::BUF - k * G::HA), rofs, k,
+                        cin - qt * kChunk);
+        writeOutputs<N, COW, HALF>(acc, ep, false, y, b, cout, cb0, pg0, k, n16, relu);
+    }
 }
 
 // The residual tower's convolutions (input in channel quads) and the
@@ -548,12 +715,20 @@ __device__ __forceinline__ void conv3x3Body(const float* __restrict__ x, const f
         NAME(const float* __restrict__ x, const f4* __restrict__ wp, const float* __restrict__ scale,      \
              const float* __restrict__ shift, const float* skip, float* y, int cin, int cout, int nq,      \
              int coTiles, int pixTiles, int relu) {                                                        \
-        if constexpr (PPW != 0 && COW * WCO == 1)                                                           \
+        if constexpr (PPW != 0 && COW * WCO == 1) {                                                         \
             conv3x3SmallBody<N, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles,      \
                                                   pixTiles, relu);                                         \
-        else                                                                                               \
-            conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(x, wp, scale, shift, skip, y, cin, cout, nq, coTiles, \
-                                                       pixTiles, relu);                                    \
+        } else {                                                                                           \
+            __shared__ f4 lds[2 * Geo<N>::BUF];                                                            \
+            if constexpr (PLANAR && PPW == 0 && WPG == 1) {                                                \
+                if (nq <= 2 && !skip) {                                                                    \
+                    conv3x3StemWhole<N, COW, WCO>(lds, x, wp, scale, shift, y, cin, cout, nq, coTiles, relu); \
+                    return;                                                                                \
+                }                                                                                          \
+            }                                                                                              \
+            conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(lds, x, wp, scale, shift, skip, y, cin, cout, nq,     \
+                                                       coTiles, pixTiles, relu);                           \
+        }                                                                                                  \
     }
 AZH_CONV_KERNEL(conv3x3Tower, false)
 AZH_CONV_KERNEL(conv3x3Stem, true)

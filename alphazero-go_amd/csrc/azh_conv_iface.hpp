@@ -44,6 +44,9 @@ struct ConvTiling {
     int coTile() const { return 16 * coPerWave * wavesCo; }
 };
 ConvTiling chooseConvTiling(int cout, int B, int boardSize);
+// The stem's shape in a pass whose tower runs `tower` over B boards in all
+// (both halves of a split pass, which run at once).
+ConvTiling chooseStemTiling(ConvTiling tower, int cout, int B);
 inline constexpr bool operator==(const ConvTiling& a, const ConvTiling& b) {
     return a.coPerWave == b.coPerWave && a.wavesCo == b.wavesCo && a.wavesPg == b.wavesPg &&
            a.pgPerWave == b.pgPerWave;

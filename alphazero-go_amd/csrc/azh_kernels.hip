@@ -308,6 +308,19 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     return {1, 1, 4, 1};
 }
 
+ConvTiling chooseStemTiling(ConvTiling tower, int cout, int B) {
+    // The stem's whole-board body stages a board's planes once per
+    // workgroup: with eight waves (128 channels) instead of four, once per
+    // board, as soon as the batch still gives every CU a workgroup (19x19
+    // 18 -> 128 planes at 256 boards: 41.7 against 44.2 us; 18 -> 256 at
+    // 512: 157.8 against 161.6; at 128 boards, half the CUs idle: 38.6
+    // against 26.6).
+    if (tower == ConvTiling{1, 4, 1, 0} && ceilDiv(cout, kCoBlock) >= 8 &&
+        (long)B * ceilDiv(cout, 8 * kCoBlock) >= deviceCUs())
+        return {1, 8, 1, 0};
+    return tower;
+}
+
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
                          const float* skip, float* y, int B, int n, int cin, int cout, bool relu, bool planarInput,
                          ConvTiling t, hipStream_t stream) {

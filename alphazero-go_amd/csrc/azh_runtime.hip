@@ -949,8 +949,8 @@ struct azh_runner {
     // blocks, then the heads when asked; workgroup shape t (the shape
     // decides only which workgroup computes an output, never how, so a
     // part's bits are the whole batch's).
-    void launchPassPart(const PassBuffers& io, int Bp, azh::ConvTiling t, hipStream_t stream, int blocksToRun,
-                        bool heads, bool small) {
+    void launchPassPart(const PassBuffers& io, int Bp, int Bpass, azh::ConvTiling t, hipStream_t stream,
+                        int blocksToRun, bool heads, bool small) {
         const Shape& sh = shape;
         if (small) {
             // The stem, the tower and the heads in one launch.
@@ -969,7 +969,7 @@ struct azh_runner {
             return;
         }
         check(azh::launchConv3x3(io.in, weights.stem.w, weights.stem.scale, weights.stem.shift, nullptr, io.x, Bp,
-                                 sh.n, sh.P, sh.F, true, true, t, stream),
+                                 sh.n, sh.P, sh.F, true, true, azh::chooseStemTiling(t, sh.F, Bpass), stream),
               "conv3x3 (stem)");
         launchTowerOn(io.x, io.mid, Bp, t, stream, blocksToRun);
         if (heads)
@@ -1095,7 +1095,7 @@ struct azh_runner {
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
         const bool small = useSmallTower(B);
         overHalves(s, B, stream, [&](int b0, int Bp, hipStream_t st) {
-            launchPassPart(slotBuffers(s, b0), Bp, partTiling(B, Bp), st, blocksToRun, heads, small);
+            launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp), st, blocksToRun, heads, small);
         });
     }
 
@@ -1499,7 +1499,7 @@ int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, f
         float* x = scratchOnCurrentDevice();
         float* mid = x + alignFloats(azh::quadFloats(B, sh.F, sh.A));
         float* act = mid + alignFloats(azh::quadFloats(B, sh.F, sh.A));
-        r->launchPassPart(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B,
+        r->launchPassPart(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B, B,
                           azh::chooseConvTiling(sh.F, B, sh.n), static_cast<hipStream_t>(stream), sh.blocks, true,
                           r->useSmallTower(B));
     });
@@ -1818,7 +1818,6 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
             throw Error(AZH_ERR_ARGUMENT, "hip: bad conv probe arguments");
         if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
         if (tiling < -1 || tiling >= kTilingCount) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index out of range");
-        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : kTilings[tiling];
         requireContext();
         const size_t A = (size_t)n * n;
         const std::vector<float> packed = azh::packConv3x3(w, cin, cout);
@@ -1826,8 +1825,12 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
         // 16-channel chunks is tried as a trunk activation (channel quads,
         // the tower kernel), any other as input planes (the stem kernel).
         // Outputs and residuals are channel quads; the probe's own arrays
-        // are planar, converted here.
+        // are planar, converted here. Tiling -1: the shape a pass of B
+        // gives that kernel.
         const bool planarIn = cin % azh::kChunk != 0;
+        const azh::ConvTiling t = tiling >= 0 ? kTilings[tiling]
+                                  : planarIn  ? azh::chooseStemTiling(azh::chooseConvTiling(cout, B, n), cout, B)
+                                              : azh::chooseConvTiling(cout, B, n);
         const std::vector<float> xq = planarIn ? std::vector<float>() : azh::toChannelQuads(x, B, cin, (int)A);
         const std::vector<float> kq = skip ? azh::toChannelQuads(skip, B, cout, (int)A) : std::vector<float>();
         const size_t fx = planarIn ? B * cin * A : xq.size(), fy = azh::quadFloats(B, cout, (int)A);
@@ -1905,8 +1908,11 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
         check(hipMemcpy(dw, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
         check(azh::launchConv3x3(dx, dw, ds, dh, nullptr, dy, B, n, cin, cout, true, planarIn, t, nullptr),
               "conv3x3");
+        // A tower layer adds its input (here its own output); the stem adds
+        // nothing, as in the pass.
+        float* skip = planarIn ? nullptr : dy;
         *ms = timeOnStream(nullptr, iters, [&] {
-            check(azh::launchConv3x3(dx, dw, ds, dh, dy, dy, B, n, cin, cout, true, planarIn, t, nullptr),
+            check(azh::launchConv3x3(dx, dw, ds, dh, skip, dy, B, n, cin, cout, true, planarIn, t, nullptr),
                   "conv3x3");
         });
     });

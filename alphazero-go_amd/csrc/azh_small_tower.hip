@@ -13,6 +13,7 @@
 // the bits the per-layer launches give it.
 #include "azh_kernels.hpp"
 #include "azh_heads.hpp"
+#include "azh_stem.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -192,12 +193,26 @@ __global__ __launch_bounds__(smallThreads<N>()) void smallTowerKernel(float* __r
 #pragma unroll
             for (int j = 0; j < PGW; ++j) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             const int nqs = GS / 4;
-            for (int q = 0; q < nqs; ++q) {
+            // The last chunk, unless the planes fill it, as the stem kernel
+            // multiplies it (stemTail).
+            const bool tail = stem.planes % kChunk != 0;
+            for (int q = 0; q < (tail ? nqs - 1 : nqs); ++q) {
                 f4 fs[9];
                 const f4* w = reinterpret_cast<const f4*>(stem.w) + (size_t)((cb * nqs + q) * 9) * 64 + lane;
 #pragma unroll
                 for (int t = 0; t < 9; ++t) fs[t] = w[t * 64];
                 multiply(fs, tm, q);
+            }
+            if (tail) {
+                const int q = nqs - 1;
+                f4 a1[1][PGW];
+#pragma unroll
+                for (int j = 0; j < PGW; ++j) a1[0][j] = acc[j];
+                const float* wl = stem.w + (size_t)((cb * nqs + q) * 9) * 256 + n16 * 4;
+                stemTail<1, PGW, HA, H>(a1, wl, 0, reinterpret_cast<const float*>(tm + 4 * q * HA), base, k,
+                                        stem.planes - q * kChunk);
+#pragma unroll
+                for (int j = 0; j < PGW; ++j) acc[j] = a1[0][j];
             }
             store(stem.scale, stem.shift, tx, false);
             __syncthreads();   // x is complete and the input tile is free

@@ -74,6 +74,45 @@ def test_tilings_bitwise_identical(hip, n, cin, cout):
         assert bitwise_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("cin", [2, 4, 5, 16, 18, 20, 30, 34])
+def test_stem_last_chunk_every_tiling(hip, cin):
+    """The stem's input planes (cin not a multiple of 16 leaves a short last
+    chunk, whose (plane, tap) pairs run packed four to an MFMA: straight-line
+    for 2 planes, a step at a time otherwise; cin <= 32 on whole boards runs
+    in two halves of column groups): every tiling gives the same bits, within
+    the fp32 summation bound and maxErr <= 1e-5 of the oracle."""
+    rng = np.random.default_rng(300 + cin)
+    n, cout, B = 19, 128, 3
+    x = _rand(rng, B, cin, n * n)
+    w = (rng.standard_normal((cout, cin * 9)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
+    ones, zeros = np.ones(cout, np.float32), np.zeros(cout, np.float32)
+    outs = [hip.probe_conv3x3(x, w, ones, zeros, relu=False, tiling=t) for t in range(10)]
+    for o in outs[1:]:
+        assert bitwise_equal(o, outs[0])
+    exact, mag = conv_exact_and_bound(x, w)
+    err = np.abs(outs[0].astype(np.float64) - exact)
+    assert (err <= cin * 9 * U * mag + 1e-30).all()
+    assert O.max_err(outs[0], oracle_conv_raw(x, w)) <= 1e-5
+
+
+@pytest.mark.parametrize("tiling", [1, 4, 8])
+def test_stem_with_skip_every_body(hip, tiling):
+    """Input planes with a residual (not the network's stem, which adds
+    nothing, but the probe's contract): whole-board shapes run the one-pass
+    body then, and the fused epilogue still equals the explicit one."""
+    rng = np.random.default_rng(81)
+    n, cin, cout, B = 19, 18, 128, 2
+    x = _rand(rng, B, cin, n * n)
+    w = _rand(rng, cout, cin * 9, lo=-0.1, hi=0.1)
+    scale = _rand(rng, cout, lo=0.5, hi=2.0)
+    shift = _rand(rng, cout, lo=-0.5, hi=0.5)
+    skip = _rand(rng, B, cout, n * n)
+    raw = hip.probe_conv3x3(x, w, np.ones(cout, np.float32), np.zeros(cout, np.float32), relu=False,
+                            tiling=tiling)
+    fused = hip.probe_conv3x3(x, w, scale, shift, skip=skip, relu=True, tiling=tiling)
+    assert bitwise_equal(fused, epilogue_f32(raw, scale, shift, skip, True))
+
+
 def test_conv_batch_independent(hip):
     rng = np.random.default_rng(9)
     n, cin, cout = 19, 128, 128

@@ -251,6 +251,9 @@ def test_small_board_split_boundaries(hip, tag, B):
     (O.make_cfg(9, 2, 20, value_hidden=16, ownership=1), 6),
     (O.make_cfg(13, 2, 16), 5),
     (O.make_cfg(13, 2, 32, value_hidden=256), 101),
+    (O.make_cfg(5, 2, 32, history=1), 5),     # 4 input planes: one short chunk
+    (O.make_cfg(9, 2, 32, history=7), 8),     # 16: one whole chunk, no short one
+    (O.make_cfg(9, 2, 32, history=16), 9),    # 34: two whole chunks and 2 planes
 ])
 def test_small_tower_equals_per_layer_launches(hip, cfg, B):
     """A small board's tower in one launch (one workgroup per board, the
@@ -271,6 +274,27 @@ def test_small_tower_equals_per_layer_launches(hip, cfg, B):
         assert len(got) == len(one)
         for a, b in zip(got, one):
             assert bitwise_equal(a, b)
+
+
+@pytest.mark.parametrize("history,B", [(8, 256), (7, 256), (9, 256), (16, 256), (8, 40), (3, 5)])
+def test_input_plane_counts_parity(hip, history, B):
+    """Networks of 2H + 2 input planes around the stem's chunking (18: a
+    2-plane last chunk; 16: none; 20: 4 planes; 34: three chunks; 8: one
+    short chunk), at 19x19 on the large-batch shapes (the stem in two halves
+    of column groups) and smaller ones: logits within maxErr 5e-5 and values
+    within 5e-5 of the oracle (the random-network bar above), and a board
+    alone gives its bits in the batch."""
+    cfg = O.make_cfg(19, 1, 128, history=history)
+    net = O.random_network(cfg, 610 + history)
+    w = O.Workload(0, "planes", cfg, B, 0.3, 0.3)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B) as r:
+        got = r.infer(inp)
+        alone = r.infer(inp[B - 1:B])
+    ref = O.forward(net, inp, O.BLAS)
+    assert O.max_err(got[0], ref[0]) <= 5e-5
+    assert float(np.abs(got[1].astype(np.float64) - ref[1]).max()) <= 5e-5
+    assert bitwise_equal(alone[0][0], got[0][B - 1]) and bitwise_equal(alone[1][0], got[1][B - 1])
 
 
 def test_repeatable_and_graph_equals_eager(hip):
