@@ -100,6 +100,11 @@ def load():
             "azh_legal_moves": ([u8, C.c_int, u8, P(C.c_uint64), P(C.c_int64), C.c_int, u8], C.c_int),
             "azh_evaluate_positions": ([vp, P(Positions), C.c_int, f32, f32, u8, f32], C.c_int),
             "azh_time_positions": ([vp, P(Positions), C.c_int, C.c_int, f32], C.c_int),
+            "azh_begin_positions": ([vp, C.c_int, C.c_int, P(Positions), DONE_FN, vp], C.c_int),
+            "azh_slot_position_logits": ([vp, C.c_int], f32),
+            "azh_slot_priors": ([vp, C.c_int], f32),
+            "azh_slot_legal": ([vp, C.c_int], u8),
+            "azh_time_pipelined_positions": ([vp, P(Positions), C.c_int, C.c_int, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
             "azh_set_small_tower": ([vp, C.c_int], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
@@ -352,6 +357,42 @@ class Runner:
         _check(self.lib.azh_evaluate_positions(self.h, C.byref(pos), B, _f(logits), _f(priors), _u8(legal),
                                                _f(values)))
         return logits, priors, legal, values
+
+    def begin_positions(self, slot, done, stones, to_move, plies=None, sym=None, seen=None):
+        """azh_begin_positions: done(slot, error_or_None) from the completion
+        thread; then position_outputs(slot, B) holds the results."""
+        B, pos, keep = self._positions(stones, to_move, plies, sym, seen)
+        key = (slot, threading.get_ident(), len(self._callbacks))
+
+        def cb(user, s, err):
+            done(s, err.decode() if err else None)
+
+        fn = DONE_FN(cb)
+        self._callbacks[key] = fn   # kept alive until the runner goes (the positions are copied before the return)
+        _check(self.lib.azh_begin_positions(self.h, slot, B, C.byref(pos), fn, None))
+
+    def position_outputs(self, slot, B):
+        """(logits mapped back, priors, legal, values) of the slot's last
+        begin_positions of B positions."""
+        A1 = self.cfg.actions
+        out = []
+        for fn, dt in ((self.lib.azh_slot_position_logits, np.float32), (self.lib.azh_slot_priors, np.float32),
+                       (self.lib.azh_slot_legal, np.uint8)):
+            p = fn(self.h, slot)
+            if not p:
+                raise HipError("no positions pass on this slot")
+            out.append(np.ctypeslib.as_array(p, (B * A1,)).reshape(B, A1).astype(dt, copy=True))
+        out.append(self.values(slot, B))
+        return tuple(out)
+
+    def time_pipelined_positions(self, B, passes, stones, to_move, plies=None, sym=None, seen=None):
+        """Wall ms for `passes` positions passes of B with every slot kept
+        full through begin_positions (the same positions each time)."""
+        n, pos, keep = self._positions(stones, to_move, plies, sym, seen)
+        assert n == B
+        ms = C.c_float()
+        _check(self.lib.azh_time_pipelined_positions(self.h, C.byref(pos), B, passes, C.byref(ms)))
+        return ms.value
 
     def set_graphs(self, enabled):
         _check(self.lib.azh_set_graphs(self.h, int(enabled)))

@@ -33,8 +33,10 @@ size_t packedConv3x3Floats(int cin, int cout);
 // How a convolution launch is cut: output channels per workgroup (a
 // multiple of 16) and the resulting number of co tiles. The cut only
 // decides which workgroup computes an output, never how: every output
-// channel sums its inputs in one fixed order (chunk, tap, channel-in-chunk),
-// so results are bitwise independent of the cut and of the batch.
+// channel sums its inputs in one fixed order (chunk, tap, channel-in-chunk;
+// the stem's short last chunk of input planes in its packed (plane, tap)
+// order, azh_stem.hpp), so results are bitwise independent of the cut and
+// of the batch.
 struct ConvTiling {
     int coPerWave;   // MFMA blocks of 16 output channels per wave: 1 or 2
     int wavesCo;     // waves along the output channels (at most 128 channels per workgroup)

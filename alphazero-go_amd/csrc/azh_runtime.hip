@@ -599,6 +599,54 @@ struct GrowingBuffer {
     }
 };
 
+// Pinned host memory that grows to the largest size asked of it. Only while
+// nothing in flight reads the old block (its slot idle).
+struct PinnedBuffer {
+    void* p = nullptr;
+    size_t cap = 0;
+    void* reserve(size_t bytes) {
+        if (bytes > cap) {
+            if (p) (void)hipHostFree(p);
+            p = nullptr;
+            cap = 0;
+            check(hipHostMalloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc(positions)");
+            cap = bytes;
+        }
+        return p;
+    }
+    ~PinnedBuffer() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+// Where B positions' arrays sit, in bytes from the start of a slot's
+// positions block, packed for B (each part 256-byte aligned): the inputs
+// [0, inputEnd), then the outputs [mapped, end). Host staging and device
+// block share it, so the inputs go up in one copy and the outputs come back
+// in one. Every offset grows with B, so the block sized for maxBatch holds
+// any B's layout.
+struct PositionsLayout {
+    size_t stones, plies, turn, sym, offsets, inputEnd, mapped, priors, legal, end;
+    PositionsLayout(size_t B, size_t H, size_t A, size_t A1) {
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t o = off;
+            off += (bytes + 255) / 256 * 256;
+            return o;
+        };
+        stones = take(B * H * A);
+        plies = take(B * sizeof(int));
+        turn = take(B);
+        sym = take(B);
+        offsets = take((B + 1) * sizeof(int64_t));
+        inputEnd = off;
+        mapped = take(B * A1 * sizeof(float));
+        priors = take(B * A1 * sizeof(float));
+        legal = take(B * A1);
+        end = off;
+    }
+};
+
 // The inputs a batch of positions brings (azh_positions), checked on the
 // host before anything reaches the GPU: every index the kernels form from
 // them then stays inside its array.
@@ -643,13 +691,15 @@ struct Slot {
     unsigned long long replays = 0;
     // Set while a pass or a synchronous call holds the slot.
     std::atomic<bool> claimed{false};
-    // The positions path (azh_evaluate_positions), allocated on first use:
-    // stones [maxBatch][H][A], plies, side to move, symmetry, superko list
-    // offsets, legal [maxBatch][A+1], mapped logits and priors, and the
-    // concatenated superko hashes (grown as needed).
+    // The positions path (azh_evaluate_positions, azh_begin_positions),
+    // allocated on first use: the device block (PositionsLayout at
+    // maxBatch) and the concatenated superko hashes (grown as needed), and
+    // their pinned host sides: the inputs staged for the copy up, the
+    // hashes, and the outputs of the last azh_begin_positions (of posLastB
+    // positions; values go to hValues).
     GrowingBuffer posBytes, posSeen;
-    std::vector<int> posPlies;       // host copies the staging reads from
-    std::vector<uint8_t> posSym;
+    PinnedBuffer posIn, posSeenIn, posOut;
+    int posLastB = 0;
 
     Slot(const Shape& s, int maxBatch) {
         const size_t B = maxBatch;
@@ -1159,52 +1209,57 @@ struct azh_runner {
     }
 
     // The positions path's device arrays for B positions in slot s, staged
-    // from the caller's (checked) host arrays on the slot's stream: the
-    // batch-sized parts in one allocation at maxBatch, the superko hashes in
-    // a buffer grown as needed.
+    // from the caller's (checked) host arrays on the slot's stream: copied
+    // into the slot's pinned staging (PositionsLayout for B), then up in
+    // one copy, and the superko hashes in a second.
     PositionsOnDevice stagePositions(Slot& s, const azh_positions& pos, int B) {
         const Shape& sh = shape;
-        const size_t A = sh.A, A1 = sh.A1, H = sh.H, M = maxBatch;
+        const size_t A = sh.A, A1 = sh.A1, H = sh.H;
         checkPositions(pos.stones, (size_t)B * H * A, pos.plies, pos.to_move, pos.sym, pos.seen_offsets, pos.seen, B,
                        sh.H);
-        size_t off = 0;
-        auto take = [&](size_t bytes) {
-            const size_t o = off;
-            off += (bytes + 255) / 256 * 256;
-            return o;
-        };
-        const size_t oStones = take(M * H * A), oPlies = take(M * sizeof(int)), oTurn = take(M), oSym = take(M),
-                     oOff = take((M + 1) * sizeof(int64_t)), oLegal = take(M * A1),
-                     oMapped = take(M * A1 * sizeof(float)), oPriors = take(M * A1 * sizeof(float));
-        uint8_t* base = static_cast<uint8_t*>(s.posBytes.reserve(off));
+        const PositionsLayout L(B, H, A, A1);
+        uint8_t* dev = static_cast<uint8_t*>(s.posBytes.reserve(PositionsLayout(maxBatch, H, A, A1).end));
+        uint8_t* host = static_cast<uint8_t*>(s.posIn.reserve(PositionsLayout(maxBatch, H, A, A1).inputEnd));
         const size_t nSeen = (size_t)pos.seen_offsets[B];
         uint64_t* seen = static_cast<uint64_t*>(s.posSeen.reserve(std::max<size_t>(nSeen, 1) * sizeof(uint64_t)));
-        s.posPlies.assign(B, sh.H);
-        if (pos.plies) std::copy(pos.plies, pos.plies + B, s.posPlies.begin());
-        s.posSym.assign(B, 0);
-        if (pos.sym) std::copy(pos.sym, pos.sym + B, s.posSym.begin());
-        auto up = [&](size_t o, const void* src, size_t bytes) {
-            check(hipMemcpyAsync(base + o, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(positions)");
-        };
-        up(oStones, pos.stones, (size_t)B * H * A);
-        up(oPlies, s.posPlies.data(), (size_t)B * sizeof(int));
-        up(oTurn, pos.to_move, B);
-        up(oSym, s.posSym.data(), B);
-        up(oOff, pos.seen_offsets, (size_t)(B + 1) * sizeof(int64_t));
-        if (nSeen)
-            check(hipMemcpyAsync(seen, pos.seen, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice, s.stream),
+        std::memcpy(host + L.stones, pos.stones, (size_t)B * H * A);
+        int* plies = reinterpret_cast<int*>(host + L.plies);
+        if (pos.plies)
+            std::memcpy(plies, pos.plies, (size_t)B * sizeof(int));
+        else
+            std::fill(plies, plies + B, sh.H);
+        std::memcpy(host + L.turn, pos.to_move, B);
+        if (pos.sym)
+            std::memcpy(host + L.sym, pos.sym, B);
+        else
+            std::memset(host + L.sym, 0, B);
+        std::memcpy(host + L.offsets, pos.seen_offsets, (size_t)(B + 1) * sizeof(int64_t));
+        check(hipMemcpyAsync(dev, host, L.inputEnd, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(positions)");
+        if (nSeen) {
+            uint64_t* seenHost = static_cast<uint64_t*>(s.posSeenIn.reserve(nSeen * sizeof(uint64_t)));
+            std::memcpy(seenHost, pos.seen, nSeen * sizeof(uint64_t));
+            check(hipMemcpyAsync(seen, seenHost, nSeen * sizeof(uint64_t), hipMemcpyHostToDevice, s.stream),
                   "hipMemcpyAsync(seen)");
+        }
         PositionsOnDevice d;
-        d.stones = base + oStones;
-        d.plies = reinterpret_cast<const int*>(base + oPlies);
-        d.turn = base + oTurn;
-        d.sym = base + oSym;
-        d.offsets = reinterpret_cast<const long long*>(base + oOff);
+        d.stones = dev + L.stones;
+        d.plies = reinterpret_cast<const int*>(dev + L.plies);
+        d.turn = dev + L.turn;
+        d.sym = dev + L.sym;
+        d.offsets = reinterpret_cast<const long long*>(dev + L.offsets);
         d.seen = seen;
-        d.legal = base + oLegal;
-        d.mapped = reinterpret_cast<float*>(base + oMapped);
-        d.priors = reinterpret_cast<float*>(base + oPriors);
+        d.legal = dev + L.legal;
+        d.mapped = reinterpret_cast<float*>(dev + L.mapped);
+        d.priors = reinterpret_cast<float*>(dev + L.priors);
         return d;
+    }
+    // The positions path on staged positions: encoding, the pass, the
+    // legal moves, the mapped logits and the priors, on the slot's stream.
+    void positionsChain(Slot& s, const PositionsOnDevice& d, int B) {
+        encodeStep(s, d, B);
+        enqueuePass(s, B);
+        legalStep(s, d, B);
+        priorsStep(s, d, B);
     }
     // encodePlanes into the pass's input.
     void encodeStep(Slot& s, const PositionsOnDevice& d, int B) {
@@ -1227,9 +1282,13 @@ struct azh_runner {
                              s.stream),
               "hipMemcpyAsync(input)");
     }
-    void copyOut(Slot& s, int B) {
+    // The test hook's hold before a pass's outputs are copied back.
+    void copyOutDelay(Slot& s) {
         const int delayUs = gHooks.copyOutDelayUs.load();
         if (delayUs > 0) check(azh::launchSpin(1000ull * delayUs, s.stream), "spin");
+    }
+    void copyOut(Slot& s, int B) {
+        copyOutDelay(s);
         check(hipMemcpyAsync(s.hLogits, s.dLogits, (size_t)B * shape.A1 * sizeof(float), hipMemcpyDeviceToHost,
                              s.stream),
               "hipMemcpyAsync(logits)");
@@ -1278,6 +1337,118 @@ void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, i
 }
 
 // ---------------------------------------------------------------- C ABI
+
+namespace {
+
+// Claims an idle slot, runs enqueue(slot) (copies and kernels on its
+// stream), records the slot's event and hands the pass to the reporter. From
+// the claim on, done is called exactly once, by the reporter, which also
+// releases the claim: an error while enqueueing travels through it, as a
+// failed pass.
+template <class Enqueue>
+void beginOnSlot(azh_runner* r, int slot, azh_done_fn done, void* user, Enqueue enqueue) {
+    Slot& s = r->slotAt(slot);
+    bool idle = false;
+    if (!s.claimed.compare_exchange_strong(idle, true))
+        throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
+    std::string error;
+    try {
+        enqueue(s);
+        check(hipEventRecord(s.event, s.stream), "hipEventRecord");
+    } catch (const std::exception& e) {
+        error = e.what();
+        if (error.empty()) error = "hip: enqueue failed";
+        (void)hipEventRecord(s.event, s.stream);
+    }
+    Reporter::Notice notice;
+    notice.slot = slot;
+    notice.event = s.event;
+    notice.claim = &s.claimed;
+    notice.done = done;
+    notice.user = user;
+    notice.error = std::move(error);
+    try {
+        r->reporter.post(std::move(notice));
+    } catch (...) {
+        s.claimed.store(false);   // never handed over: no done will come
+        throw;
+    }
+}
+
+} // namespace
+
+namespace {
+
+// The last azh_begin_positions' outputs in the slot's pinned block (NULL
+// before the slot's first).
+const uint8_t* positionOutputs(const azh_runner* r, int slot, size_t PositionsLayout::*part) {
+    if (!r || slot < 0 || slot >= (int)r->slots.size()) return nullptr;
+    const Slot& s = *r->slots[slot];
+    if (!s.posOut.p || s.posLastB < 1) return nullptr;
+    const Shape& sh = r->shape;
+    const PositionsLayout L(s.posLastB, sh.H, sh.A, sh.A1);
+    return static_cast<const uint8_t*>(s.posOut.p) + (L.*part - L.mapped);
+}
+
+} // namespace
+
+namespace {
+
+// Keeps every slot of r busy through begin(slot, done, user) (one pass in
+// flight per slot, each resubmitted as soon as its done comes) until
+// `passes` have completed; wall ms from the first begin to the last done.
+// A pass that fails stops the resubmission; the passes in flight are drained
+// and the error is thrown.
+template <class Begin>
+float keepFull(azh_runner* r, int passes, Begin begin) {
+    const int slots = azh_slots(r);
+    for (int i = 0; i < slots; ++i) r->claimIdle(i);   // each idle now (claimed and released)
+    // The done handler's state outlives every pass it is handed to: all
+    // of them are drained before this function returns.
+    struct Done {
+        std::mutex m;
+        std::condition_variable cv;
+        std::vector<int> ready;
+        std::string error;
+    } st;
+    const azh_done_fn done = [](void* user, int slot, const char* error) {
+        Done* d = static_cast<Done*>(user);
+        std::lock_guard<std::mutex> lock(d->m);
+        if (error && *error && d->error.empty()) d->error = error;
+        d->ready.push_back(slot);
+        d->cv.notify_one();
+    };
+    int inFlight = 0, begun = 0;
+    auto start = [&](int slot) {
+        if (begin(slot, done, &st) != AZH_OK) {
+            std::lock_guard<std::mutex> lock(st.m);
+            if (st.error.empty()) st.error = azh_last_error();
+            return;
+        }
+        ++inFlight;
+        ++begun;
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < slots && begun < passes; ++i) start(i);
+    while (inFlight > 0) {
+        int slot;
+        bool failed;
+        {
+            std::unique_lock<std::mutex> lock(st.m);
+            st.cv.wait(lock, [&] { return !st.ready.empty(); });
+            slot = st.ready.back();
+            st.ready.pop_back();
+            failed = !st.error.empty();
+        }
+        --inFlight;
+        if (!failed && begun < passes) start(slot);
+    }
+    const float ms = (float)std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    if (!st.error.empty()) throw Error(AZH_ERR_HIP, st.error);
+    return ms;
+}
+
+} // namespace
 
 extern "C" {
 
@@ -1415,41 +1586,52 @@ const float* azh_slot_values(const azh_runner* r, int slot) {
     return r && slot >= 0 && slot < (int)r->slots.size() ? r->slots[slot]->hValues : nullptr;
 }
 
+const float* azh_slot_position_logits(const azh_runner* r, int slot) {
+    return reinterpret_cast<const float*>(positionOutputs(r, slot, &PositionsLayout::mapped));
+}
+
+const float* azh_slot_priors(const azh_runner* r, int slot) {
+    return reinterpret_cast<const float*>(positionOutputs(r, slot, &PositionsLayout::priors));
+}
+
+const uint8_t* azh_slot_legal(const azh_runner* r, int slot) {
+    return positionOutputs(r, slot, &PositionsLayout::legal);
+}
+
 int azh_begin(azh_runner* r, int slot, int B, azh_done_fn done, void* user) {
     return guarded([&] {
         if (!r || !done) throw Error(AZH_ERR_ARGUMENT, "hip: begin needs a runner and a done callback");
         r->checkBatch(B);
-        Slot& s = r->slotAt(slot);
-        bool idle = false;
-        if (!s.claimed.compare_exchange_strong(idle, true))
-            throw Error(AZH_ERR_STATE, "hip: slot " + std::to_string(slot) + " has a pass in flight");
-        // From here done is called exactly once, by the reporter, which also
-        // releases the claim: errors while enqueueing travel through it, as
-        // a failed pass.
-        std::string error;
-        try {
+        beginOnSlot(r, slot, done, user, [&](Slot& s) {
             r->copyIn(s, B);
             r->enqueuePass(s, B);
             r->copyOut(s, B);
-            check(hipEventRecord(s.event, s.stream), "hipEventRecord");
-        } catch (const std::exception& e) {
-            error = e.what();
-            if (error.empty()) error = "hip: enqueue failed";
-            (void)hipEventRecord(s.event, s.stream);
-        }
-        Reporter::Notice notice;
-        notice.slot = slot;
-        notice.event = s.event;
-        notice.claim = &s.claimed;
-        notice.done = done;
-        notice.user = user;
-        notice.error = std::move(error);
-        try {
-            r->reporter.post(std::move(notice));
-        } catch (...) {
-            s.claimed.store(false);   // never handed over: no done will come
-            throw;
-        }
+        });
+    });
+}
+
+int azh_begin_positions(azh_runner* r, int slot, int B, const azh_positions* pos, azh_done_fn done, void* user) {
+    return guarded([&] {
+        if (!r || !pos || !done)
+            throw Error(AZH_ERR_ARGUMENT, "hip: begin_positions needs a runner, positions and a done callback");
+        r->checkBatch(B);
+        const Shape& sh = r->shape;
+        // Checked here, so that bad positions fail the call, before the claim.
+        checkPositions(pos->stones, (size_t)B * sh.H * sh.A, pos->plies, pos->to_move, pos->sym, pos->seen_offsets,
+                       pos->seen, B, sh.H);
+        beginOnSlot(r, slot, done, user, [&](Slot& s) {
+            const PositionsOnDevice d = r->stagePositions(s, *pos, B);
+            r->positionsChain(s, d, B);
+            const PositionsLayout L(B, sh.H, sh.A, sh.A1);
+            const PositionsLayout M(r->maxBatch, sh.H, sh.A, sh.A1);
+            void* out = s.posOut.reserve(M.end - M.mapped);
+            s.posLastB = B;
+            r->copyOutDelay(s);
+            check(hipMemcpyAsync(out, d.mapped, L.end - L.mapped, hipMemcpyDeviceToHost, s.stream),
+                  "hipMemcpyAsync(position outputs)");
+            check(hipMemcpyAsync(s.hValues, s.dValues, (size_t)B * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+                  "hipMemcpyAsync(values)");
+        });
     });
 }
 
@@ -1595,10 +1777,7 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
         const SlotClaim held = r->claimIdle(0);
         Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
-        r->encodeStep(s, d, B);
-        r->enqueuePass(s, B);
-        r->legalStep(s, d, B);
-        r->priorsStep(s, d, B);
+        r->positionsChain(s, d, B);
         const size_t A1 = r->shape.A1;
         auto down = [&](void* dst, const void* src, size_t bytes) {
             check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync(outputs)");
@@ -1619,10 +1798,7 @@ int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters
         Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
         // One untimed run of everything (the pass's graph for B is captured here).
-        r->encodeStep(s, d, B);
-        r->enqueuePass(s, B);
-        r->legalStep(s, d, B);
-        r->priorsStep(s, d, B);
+        r->positionsChain(s, d, B);
         hipEvent_t e0 = nullptr, e1 = nullptr;
         check(hipEventCreate(&e0), "hipEventCreate");
         check(hipEventCreate(&e1), "hipEventCreate");
@@ -1764,50 +1940,18 @@ int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms) {
     return guarded([&] {
         if (!r || !ms || passes < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
         r->checkBatch(B);
-        const int slots = azh_slots(r);
-        for (int i = 0; i < slots; ++i) r->claimIdle(i);   // each idle now (claimed and released)
-        // The done handler's state outlives every pass it is handed to: all
-        // of them are drained before this function returns.
-        struct Done {
-            std::mutex m;
-            std::condition_variable cv;
-            std::vector<int> ready;
-            std::string error;
-        } st;
-        const azh_done_fn done = [](void* user, int slot, const char* error) {
-            Done* d = static_cast<Done*>(user);
-            std::lock_guard<std::mutex> lock(d->m);
-            if (error && *error && d->error.empty()) d->error = error;
-            d->ready.push_back(slot);
-            d->cv.notify_one();
-        };
-        int inFlight = 0, begun = 0;
-        auto begin = [&](int slot) {
-            if (azh_begin(r, slot, B, done, &st) != AZH_OK) {
-                std::lock_guard<std::mutex> lock(st.m);
-                if (st.error.empty()) st.error = azh_last_error();
-                return;
-            }
-            ++inFlight;
-            ++begun;
-        };
-        const auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < slots && begun < passes; ++i) begin(i);
-        while (inFlight > 0) {
-            int slot;
-            bool failed;
-            {
-                std::unique_lock<std::mutex> lock(st.m);
-                st.cv.wait(lock, [&] { return !st.ready.empty(); });
-                slot = st.ready.back();
-                st.ready.pop_back();
-                failed = !st.error.empty();
-            }
-            --inFlight;
-            if (!failed && begun < passes) begin(slot);
-        }
-        *ms = (float)std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        if (!st.error.empty()) throw Error(AZH_ERR_HIP, st.error);
+        *ms = keepFull(r, passes,
+                       [&](int slot, azh_done_fn done, void* user) { return azh_begin(r, slot, B, done, user); });
+    });
+}
+
+int azh_time_pipelined_positions(azh_runner* r, const azh_positions* pos, int B, int passes, float* ms) {
+    return guarded([&] {
+        if (!r || !pos || !ms || passes < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        r->checkBatch(B);
+        *ms = keepFull(r, passes, [&](int slot, azh_done_fn done, void* user) {
+            return azh_begin_positions(r, slot, B, pos, done, user);
+        });
     });
 }
 

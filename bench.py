@@ -180,10 +180,14 @@ def stem_heads(workload, B, iters):
                       "stem_us_per_launch": round(ms * 1e3, 2)}), flush=True)
 
 
-def positions_leg(r, w, B, seen_per_position, iters=20):
+def positions_leg(r, w, B, seen_per_position, iters=20, passes=None):
     """The positions path on the benchmark's boards (no history: ply 0 only),
     device-resident: HIP events around each step (encode, legal moves,
-    priors) and the whole chain (encode, pass, legal moves, priors)."""
+    priors) and the whole chain (encode, pass, legal moves, priors); and
+    with `passes`, the runner kept full through azh_begin_positions (every
+    slot with a positions pass in flight: stone bytes and superko hashes up,
+    logits, priors, legal actions and values back, through pinned
+    staging)."""
     import numpy as np
     import workload as W
     n, H = w.cfg[0], w.cfg[1]
@@ -198,6 +202,14 @@ def positions_leg(r, w, B, seen_per_position, iters=20):
     A, P = n * n, 2 * H + 2
     enc_bytes = B * (H * A + P * A * 4)                      # stone bytes in, planes out
     leg_bytes = B * (A + (A + 1) + 8 * seen_per_position)    # boards and superko hashes in, masks out
+    kept = {}
+    if passes:
+        r.time_pipelined_positions(B, 4, hist, tm, plies, sym, seen)   # every slot's graph captured
+        ms = r.time_pipelined_positions(B, passes, hist, tm, plies, sym, seen)
+        kept = {"kept_full_positions_per_s": round(B * passes / (ms * 1e-3), 1),
+                "kept_full_passes": passes,
+                "host_bytes_in_per_position": H * A + 4 + 1 + 1 + 8 + 8 * seen_per_position,
+                "planes_bytes_per_position": P * A * 4}
     return {
         "workload": f"{n}x{n} batch {B}, the benchmark's boards, {seen_per_position} superko hashes each",
         "encode_us": round(enc * 1e3, 2),
@@ -208,6 +220,7 @@ def positions_leg(r, w, B, seen_per_position, iters=20):
         "encode_gbs": round(enc_bytes / (enc * 1e-3) / 1e9, 1),
         "legal_positions_per_s": round(B / (leg * 1e-3), 1),
         "legal_gbs": round(leg_bytes / (leg * 1e-3) / 1e9, 2),
+        **kept,
         "_inputs": (st, tm, seen),
     }
 
@@ -312,7 +325,8 @@ def main():
             two_slot = round(B * pipe_passes / (r.time_pipelined(B, pipe_passes) * 1e-3), 1)
         logits, values = r.fetch(0, B)
         assert (logits == logits).all() and (values == values).all(), "NaN in outputs"
-        pos = None if args.no_positions else positions_leg(r, w, B, args.seen)
+        pos = None if args.no_positions else positions_leg(
+            r, w, B, args.seen, passes=None if args.no_two_slot else max(8, args.steps))
 
     # One launch runs layers_per_launch layers of the tower (one).
     conv_flops = w.trunk_conv_flops(B) * layers_per_launch

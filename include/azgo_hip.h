@@ -252,6 +252,27 @@ typedef struct azh_positions {
 int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float* logits, float* priors,
                            uint8_t* legal, float* values);
 
+/* azh_evaluate_positions as an asynchronous pass on a slot, as azh_begin
+ * runs azh_infer's (the positions path of Mcts::evaluateLeaves and
+ * Mcts::expand, src/mcts.cpp:113-183, behind the hub's BatchRunner::begin,
+ * src/inference_hub.cpp:222-227): the arrays of `pos` are checked, copied
+ * into the slot's pinned staging (H stone bytes per point, not 2H+2 input
+ * floats) and the call returns once the copies and kernels are enqueued;
+ * done(user, slot, error) follows from the completion thread once the
+ * outputs are in the slot's pinned buffers: azh_slot_position_logits,
+ * azh_slot_priors, azh_slot_legal ([B][n*n+1] each) and azh_slot_values
+ * ([B]), valid until the slot's next begin. Bad positions (as
+ * azh_evaluate_positions checks them), a B outside [1, max_batch] or a
+ * busy slot fail here, before anything is enqueued. Same kernels, same bits
+ * as azh_evaluate_positions. The slot's positions buffers (device and
+ * pinned) are allocated on its first positions call. */
+int azh_begin_positions(azh_runner* r, int slot, int B, const azh_positions* pos, azh_done_fn done, void* user);
+/* The outputs of the slot's last azh_begin_positions (NULL before its first):
+ * logits mapped back from each position's symmetry, priors, legal. */
+const float* azh_slot_position_logits(const azh_runner* r, int slot);
+const float* azh_slot_priors(const azh_runner* r, int slot);
+const uint8_t* azh_slot_legal(const azh_runner* r, int slot);
+
 /* HIP events on slot 0's stream around `iters` device-resident runs of each
  * step of azh_evaluate_positions, on positions staged once: ms[0] the
  * encoding, ms[1] the legal moves, ms[2] the priors, ms[3] the whole chain
@@ -313,6 +334,11 @@ int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
  * first begin to the last done. A pass that fails stops the resubmission;
  * the passes in flight are drained and the error is returned. */
 int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms);
+
+/* azh_time_pipelined for the positions path: every slot kept full through
+ * azh_begin_positions on the same positions `pos` (B of them; host copies of
+ * stone bytes in, logits, priors, legal actions and values out). */
+int azh_time_pipelined_positions(azh_runner* r, const azh_positions* pos, int B, int passes, float* ms);
 
 /* ---------------------------------------------------------------- kernel probes (tests) */
 

@@ -201,3 +201,91 @@ def test_time_positions_runs_each_step(hip):
         # the slot is idle again: an evaluation after the timing works
         logits, priors, legal, values = r.evaluate_positions(stones, to_move)
     assert np.isfinite(logits).all() and np.isfinite(values).all()
+
+
+def _game_positions(n, H, B, seed):
+    """B game positions of board n with history, random symmetries and their
+    superko lists (as test_evaluate_positions_end_to_end draws them)."""
+    g = np.random.default_rng(seed)
+    pos = [(n_, s, st, tm, hs, lg) for (n_, s, st, tm, hs, lg) in games() if n_ == n]
+    hist, plies, to_move, sym, seen = [], [], [], [], []
+    for b in range(B):
+        _, _, st, tm, hs, lg = pos[b % len(pos)]
+        i = int(g.integers(0, len(st)))
+        h, k = _history(st, i, H)
+        hist.append(h)
+        plies.append(k)
+        to_move.append(tm[i])
+        sym.append(g.integers(0, 8))
+        seen.append(hs[:i + 1])
+    return (np.stack(hist), np.array(to_move, np.uint8), np.array(plies, np.int32), np.array(sym, np.uint8), seen)
+
+
+@pytest.mark.parametrize("n,tag", [(9, "2"), (19, "3")])
+def test_begin_positions_equals_evaluate(hip, n, tag):
+    """azh_begin_positions (asynchronous, per-slot pinned stone staging)
+    gives azh_evaluate_positions' outputs bit for bit: two slots in flight at
+    once on different batches, then a smaller batch on a slot that held a
+    larger one (the outputs' packing follows the batch size)."""
+    import threading
+    net = calibrated_network(tag)
+    H = net.cfg.history
+    B = 24 if n < 19 else 16
+    first = _game_positions(n, H, B, 40 + n)
+    second = _game_positions(n, H, B, 50 + n)
+    small = tuple(a[:5] if isinstance(a, np.ndarray) else a[:5] for a in second)
+    with hip.Runner(to_hip_cfg(hip, net.cfg), net.tensors(), B, 2) as r:
+        want = [r.evaluate_positions(*first), r.evaluate_positions(*second), r.evaluate_positions(*small)]
+        events = [threading.Event(), threading.Event()]
+        errors = []
+
+        def done(slot, err):
+            if err:
+                errors.append(err)
+            events[slot].set()
+
+        r.begin_positions(0, done, *first)
+        r.begin_positions(1, done, *second)
+        for e in events:
+            assert e.wait(60)
+        assert not errors, errors
+        got = [r.position_outputs(0, B), r.position_outputs(1, B)]
+        events[0].clear()
+        r.begin_positions(0, done, *small)
+        assert events[0].wait(60) and not errors
+        got.append(r.position_outputs(0, 5))
+    for g_, w_ in zip(got, want):
+        # logits mapped back, priors, legal, values
+        for a, b in zip(g_, (w_[0], w_[1], w_[2], w_[3])):
+            assert a.shape == b.shape and a.tobytes() == b.tobytes()
+
+
+def test_begin_positions_refusals(hip):
+    """Bad positions fail the call before the slot is claimed (the slot
+    stays usable), as does a busy slot; the pass after them is right."""
+    import threading
+    net = calibrated_network("1")
+    n, H, B = 5, net.cfg.history, 6
+    stones, to_move, plies, sym, seen = _game_positions(n, H, B, 77)
+    with hip.Runner(to_hip_cfg(hip, net.cfg), net.tensors(), B, 1) as r:
+        want = r.evaluate_positions(stones, to_move, plies, sym, seen)
+        ev = threading.Event()
+        bad = stones.copy()
+        bad[0, 0, 0] = 3
+        with pytest.raises(hip.HipError, match="stone byte"):
+            r.begin_positions(0, lambda s, e: ev.set(), bad, to_move, plies, sym, seen)
+        bad_turn = to_move.copy()
+        bad_turn[1] = 0
+        with pytest.raises(hip.HipError, match="side to move"):
+            r.begin_positions(0, lambda s, e: ev.set(), stones, bad_turn, plies, sym, seen)
+        hip.set_copy_out_delay(200000)   # the pass holds the slot for 0.2 s
+        try:
+            r.begin_positions(0, lambda s, e: ev.set(), stones, to_move, plies, sym, seen)
+            with pytest.raises(hip.HipError, match="in flight"):
+                r.begin_positions(0, lambda s, e: None, stones, to_move, plies, sym, seen)
+            assert ev.wait(60)
+        finally:
+            hip.set_copy_out_delay(0)
+        got = r.position_outputs(0, B)
+    for a, b in zip(got, want):
+        assert a.tobytes() == b.tobytes()
