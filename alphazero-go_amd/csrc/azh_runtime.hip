@@ -2016,7 +2016,11 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
             throw Error(AZH_ERR_ARGUMENT, "hip: bad conv timing arguments");
         if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
         if (tiling < -1 || tiling >= kTilingCount) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index out of range");
-        const azh::ConvTiling t = tiling < 0 ? azh::chooseConvTiling(cout, B, n) : kTilings[tiling];
+        const bool planarIn = cin % azh::kChunk != 0;   // as azh_probe_conv3x3 chooses
+        // Tiling -1: the shape a pass of B gives that kernel.
+        const azh::ConvTiling t = tiling >= 0 ? kTilings[tiling]
+                                  : planarIn  ? azh::chooseStemTiling(azh::chooseConvTiling(cout, B, n), cout, B)
+                                              : azh::chooseConvTiling(cout, B, n);
         requireContext();
         const size_t A = (size_t)n * n;
         std::vector<float> w((size_t)cout * cin * 9);
@@ -2039,7 +2043,6 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
             bufs.push_back(p);
             return p;
         };
-        const bool planarIn = cin % azh::kChunk != 0;   // as azh_probe_conv3x3 chooses
         const size_t fx = planarIn ? B * cin * A : azh::quadFloats(B, cin, (int)A);
         float* dx = dev(fx);
         float* dw = dev(packed.size());
