@@ -653,8 +653,9 @@ struct PositionsLayout {
 void checkPositions(const uint8_t* stones, size_t stoneBytes, const int32_t* plies, const uint8_t* toMove,
                     const uint8_t* sym, const int64_t* seenOffsets, const uint64_t* seen, int B, int H) {
     if (!stones || !toMove || !seenOffsets) throw Error(AZH_ERR_ARGUMENT, "hip: positions need stones, to_move and seen_offsets");
-    for (size_t i = 0; i < stoneBytes; ++i)
-        if (stones[i] > 2) throw Error(AZH_ERR_ARGUMENT, "hip: a stone byte is not Empty (0), Black (1) or White (2)");
+    uint8_t top = 0;   // the largest byte: one vectorisable pass, no early exit
+    for (size_t i = 0; i < stoneBytes; ++i) top = std::max(top, stones[i]);
+    if (top > 2) throw Error(AZH_ERR_ARGUMENT, "hip: a stone byte is not Empty (0), Black (1) or White (2)");
     for (int b = 0; b < B; ++b) {
         if (toMove[b] != 1 && toMove[b] != 2)
             throw Error(AZH_ERR_ARGUMENT, "hip: position " + std::to_string(b) + " has no side to move (1 or 2)");
@@ -1208,15 +1209,19 @@ struct azh_runner {
         check(hipGraphLaunch(it->second.exec, s.stream), "hipGraphLaunch");
     }
 
+    // Checks B positions' host arrays (checkPositions) for this network.
+    void checkPositionsFor(const azh_positions& pos, int B) const {
+        checkPositions(pos.stones, (size_t)B * shape.H * shape.A, pos.plies, pos.to_move, pos.sym, pos.seen_offsets,
+                       pos.seen, B, shape.H);
+    }
     // The positions path's device arrays for B positions in slot s, staged
-    // from the caller's (checked) host arrays on the slot's stream: copied
-    // into the slot's pinned staging (PositionsLayout for B), then up in
-    // one copy, and the superko hashes in a second.
+    // from the caller's host arrays, checked beforehand (checkPositionsFor),
+    // on the slot's stream: copied into the slot's pinned staging
+    // (PositionsLayout for B), then up in one copy, and the superko hashes
+    // in a second.
     PositionsOnDevice stagePositions(Slot& s, const azh_positions& pos, int B) {
         const Shape& sh = shape;
         const size_t A = sh.A, A1 = sh.A1, H = sh.H;
-        checkPositions(pos.stones, (size_t)B * H * A, pos.plies, pos.to_move, pos.sym, pos.seen_offsets, pos.seen, B,
-                       sh.H);
         const PositionsLayout L(B, H, A, A1);
         uint8_t* dev = static_cast<uint8_t*>(s.posBytes.reserve(PositionsLayout(maxBatch, H, A, A1).end));
         uint8_t* host = static_cast<uint8_t*>(s.posIn.reserve(PositionsLayout(maxBatch, H, A, A1).inputEnd));
@@ -1617,8 +1622,7 @@ int azh_begin_positions(azh_runner* r, int slot, int B, const azh_positions* pos
         r->checkBatch(B);
         const Shape& sh = r->shape;
         // Checked here, so that bad positions fail the call, before the claim.
-        checkPositions(pos->stones, (size_t)B * sh.H * sh.A, pos->plies, pos->to_move, pos->sym, pos->seen_offsets,
-                       pos->seen, B, sh.H);
+        r->checkPositionsFor(*pos, B);
         beginOnSlot(r, slot, done, user, [&](Slot& s) {
             const PositionsOnDevice d = r->stagePositions(s, *pos, B);
             r->positionsChain(s, d, B);
@@ -1774,6 +1778,7 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
         if (!r || !pos || !priors || !legal || !values)
             throw Error(AZH_ERR_ARGUMENT, "hip: evaluate_positions needs its arrays");
         r->checkBatch(B);
+        r->checkPositionsFor(*pos, B);
         const SlotClaim held = r->claimIdle(0);
         Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
@@ -1794,6 +1799,7 @@ int azh_time_positions(azh_runner* r, const azh_positions* pos, int B, int iters
     return guarded([&] {
         if (!r || !pos || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
         r->checkBatch(B);
+        r->checkPositionsFor(*pos, B);
         const SlotClaim held = r->claimIdle(0);
         Slot& s = held.slot;
         const PositionsOnDevice d = r->stagePositions(s, *pos, B);
