@@ -370,7 +370,7 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
         const int ql = nq - 1, buf = ql & 1;
         // rofs[j] - k * GC is the lane's top-left cell.
         stemTail<1, PPW, GC, G::H>(acc, reinterpret_cast<const float*>(alds + buf * AITEMS) + n16 * 4, 0,
-                                   reinterpret_cast<const float*>(lds + buf * CB - k * GC), rofs, k,
+                                   reinterpret_cast<const float*>(lds + buf * CB), rofs, k * GC, k,
                                    cin - ql * kChunk);
     }
 
@@ -553,7 +553,7 @@ __device__ __forceinline__ void conv3x3Body(f4* lds, const float* __restrict__ x
             reinterpret_cast<const float*>(wp) + (size_t)cb0 * nq * 9 * 256 + (size_t)q * 9 * 256 + n16 * 4;
         // rofs[j] - k * HA is the lane's top-left cell.
         stemTail<COW, PPW, G::HA, G::H>(acc, wl, (size_t)nq * 9 * 256,
-                                        reinterpret_cast<const float*>(lds + (q & 1) * G::BUF - k * G::HA), rofs,
+                                        reinterpret_cast<const float*>(lds + (q & 1) * G::BUF), rofs, k * G::HA,
                                         k, cin - q * kChunk);
     }
 
@@ -697,7 +697,7 @@ __device__ __forceinline__ void conv3x3StemWhole(f4* lds, const float* __restric
         }
         // rofs[j] - k * HA is the lane's top-left cell.
         if (tail)
-            st.multiply(acc, wl, blockStride, reinterpret_cast<const float*>(lds + qt * G::BUF - k * G::HA), rofs, k,
+            st.multiply(acc, wl, blockStride, reinterpret_cast<const float*>(lds + qt * G::BUF), rofs, k * G::HA, k,
                         cin - qt * kChunk);
         writeOutputs<N, COW, HALF>(acc, ep, false, y, b, cout, cb0, pg0, k, n16, relu);
     }

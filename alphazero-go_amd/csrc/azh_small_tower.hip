@@ -209,7 +209,7 @@ __global__ __launch_bounds__(smallThreads<N>()) void smallTowerKernel(float* __r
 #pragma unroll
                 for (int j = 0; j < PGW; ++j) a1[0][j] = acc[j];
                 const float* wl = stem.w + (size_t)((cb * nqs + q) * 9) * 256 + n16 * 4;
-                stemTail<1, PGW, HA, H>(a1, wl, 0, reinterpret_cast<const float*>(tm + 4 * q * HA), base, k,
+                stemTail<1, PGW, HA, H>(a1, wl, 0, reinterpret_cast<const float*>(tm + 4 * q * HA), base, 0, k,
                                         stem.planes - q * kChunk);
 #pragma unroll
                 for (int j = 0; j < PGW; ++j) acc[j] = a1[0][j];

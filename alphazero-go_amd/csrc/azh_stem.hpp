@@ -36,9 +36,10 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // wl: the chunk's fragment floats of block cb0 with the lane's row added
 // (n16 floats of 4: block c at c * blockStride floats, tap t at t * 256,
 // lane group g at g * 64); acc: the lane's COW x PPW accumulators; bq: the
-// chunk's staged quads as floats (quad g at g * GC cells), less any
-// per-lane offset that cell carries; cell: the lane's top-left tap cell per
-// column group. Global or LDS fragments alike (wl may point into LDS).
+// chunk's staged quads as floats (quad g at g * GC cells); cell[j] - bias:
+// the lane's top-left tap cell of column group j (a caller's read positions
+// may carry a per-lane offset, bias). Global or LDS fragments alike (wl may
+// point into LDS).
 template <int COW, int GC, int H>
 struct StemTail {
     static constexpr int tapOff(int t) { return (t / 3) * H + (t % 3); }
@@ -65,13 +66,14 @@ struct StemTail {
 
     template <int PPW>
     __device__ __forceinline__ void multiply(stem_detail::f4 (&acc)[COW][PPW], const float* wl, size_t blockStride,
-                                             const float* bq, const int (&cell)[PPW], int k, int rem) const {
+                                             const float* bq, const int (&cell)[PPW], int bias, int k,
+                                             int rem) const {
         if (rem == 2) {
 #pragma unroll
             for (int s = 0; s < 5; ++s)
 #pragma unroll
                 for (int j = 0; j < PPW; ++j) {
-                    const float bv = bq[cell[j] * 4 + bofs[s]];
+                    const float bv = bq[(cell[j] - bias) * 4 + bofs[s]];
 #pragma unroll
                     for (int cc = 0; cc < COW; ++cc)
                         acc[cc][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cc][s], bv, acc[cc][j], 0, 0, 0);
@@ -90,7 +92,7 @@ struct StemTail {
             for (int cc = 0; cc < COW; ++cc) a1[cc] = wl[cc * blockStride + wofs];
 #pragma unroll
             for (int j = 0; j < PPW; ++j) {
-                const float bv = bq[cell[j] * 4 + bofs1];
+                const float bv = bq[(cell[j] - bias) * 4 + bofs1];
 #pragma unroll
                 for (int cc = 0; cc < COW; ++cc)
                     acc[cc][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[cc], bv, acc[cc][j], 0, 0, 0);
@@ -102,10 +104,10 @@ struct StemTail {
 // Fetch and multiply in one call.
 template <int COW, int PPW, int GC, int H>
 __device__ __forceinline__ void stemTail(stem_detail::f4 (&acc)[COW][PPW], const float* wl, size_t blockStride,
-                                         const float* bq, const int (&cell)[PPW], int k, int rem) {
+                                         const float* bq, const int (&cell)[PPW], int bias, int k, int rem) {
     StemTail<COW, GC, H> st;
     st.fetch(wl, blockStride, k, rem);
-    st.multiply(acc, wl, blockStride, bq, cell, k, rem);
+    st.multiply(acc, wl, blockStride, bq, cell, bias, k, rem);
 }
 
 } // namespace azh
