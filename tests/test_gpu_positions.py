@@ -289,3 +289,31 @@ def test_begin_positions_refusals(hip):
         got = r.position_outputs(0, B)
     for a, b in zip(got, want):
         assert a.tobytes() == b.tobytes()
+
+
+def test_positions_kept_full_and_failure(hip):
+    """azh_time_pipelined_positions keeps both slots busy through
+    azh_begin_positions: every pass completes once and both slots hold the
+    synchronous outputs afterwards; an injected failure (the runner's
+    fail-after-n hook) comes back through done, stops the resubmission and
+    leaves both slots usable."""
+    net = calibrated_network("2")
+    n, H, B = 9, net.cfg.history, 20
+    stones, to_move, plies, sym, seen = _game_positions(n, H, B, 91)
+    with hip.Runner(to_hip_cfg(hip, net.cfg), net.tensors(), B, 2) as r:
+        want = r.evaluate_positions(stones, to_move, plies, sym, seen)
+        before = hip.passes_completed()
+        ms = r.time_pipelined_positions(B, 7, stones, to_move, plies, sym, seen)
+        assert ms > 0 and hip.passes_completed() - before == 7
+        for slot in (0, 1):
+            for a, b in zip(r.position_outputs(slot, B), want):
+                assert a.tobytes() == b.tobytes()
+        hip.fail_passes_after(2)
+        try:
+            with pytest.raises(hip.HipError, match="injected failure"):
+                r.time_pipelined_positions(B, 12, stones, to_move, plies, sym, seen)
+        finally:
+            hip.fail_passes_after(0)
+        assert r.time_pipelined_positions(B, 2, stones, to_move, plies, sym, seen) > 0
+        for a, b in zip(r.position_outputs(0, B), want):
+            assert a.tobytes() == b.tobytes()
