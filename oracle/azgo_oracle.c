@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product (the HIP library under
  * alphazero-go_amd/) links, loads or calls this file; only tests/, the smoke
- * check and the bench's CPU-baseline leg use it, as the checker.
+ * check and the bench's CPU-baseline leg use it, to check results against.
  *
  * Every function cites the reference file:line it follows (paths relative to
  * the reference repository). Compiled with -ffp-contract=off, as the

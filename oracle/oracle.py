@@ -2,7 +2,7 @@
 reference's own sources in _ref/libazgo_ref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check and by the
-bench's CPU-baseline leg, as the checker. The product (the HIP library and its
+bench's CPU-baseline leg, to check results against. The product (the HIP library and its
 binding under alphazero-go_amd/) never imports it.
 
 The benchmark workloads (the five network/batch configurations the

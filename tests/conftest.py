@@ -1,4 +1,4 @@
-"""Test setup: the `gpu` marker, import paths for the oracle (the checker)
+"""Test setup: the `gpu` marker, import paths for the oracle (what results are checked against)
 and the backend's Python binding, and shared fixtures."""
 import os
 import sys
@@ -20,7 +20,7 @@ def pytest_configure(config):
 def _ensure_built():
     """Builds what the tests load when a fresh checkout lacks it: the oracle
     (gcc, seconds), the workload generator (g++) and, where hipcc exists, the
-    HIP library. A GPU box receives them prebuilt."""
+    HIP library. A machine without the toolchain needs them prebuilt."""
     import subprocess
     if not os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
         subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "oracle"], check=True)

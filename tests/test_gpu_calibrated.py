@@ -3,7 +3,7 @@ makes them: Network(cfg, 1)'s weights with the batch-norm running
 statistics of calibrateBatchNorm (src/bn_calibration.cpp:33-45, the
 trainer's seed, src/trainer.cpp:559; tests/golden/calibrated_bn.npz). These
 are normalised networks (|logit| of a few units, values inside (-1, 1)), so
-the north-star bar applies as written, at every benchmark shape including
+the parity bar applies as written, at every benchmark shape including
 the 19x19 headline: max-abs 1e-4 on logits and on values against the blas
 restatement of Network::infer, and argmax agreement over legal moves of at
 least 99.9%.
@@ -22,7 +22,7 @@ from _util import GOLDEN, calibrated_network, parity_report, to_hip_cfg, bitwise
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-4   # max-abs on logits and values
+TOL = 1e-4   # max-abs on logits and values (the parity bar)
 
 # (calibration tag, network config, GPU batch, positions checked on the CPU).
 # The 20x256 net's pass runs at its benchmark batch of 512; the CPU checks a
@@ -50,7 +50,7 @@ def _workload_for(cfg):
 
 @pytest.mark.parametrize("tag,cfg,B,check", CASES,
                          ids=[f"{c[0]}-b{c[2]}" for c in CASES])
-def test_calibrated_parity_north_star(hip, tag, cfg, B, check):
+def test_calibrated_parity(hip, tag, cfg, B, check):
     net = calibrated_network(tag, cfg)
     w = _workload_for(cfg)
     inp, legal = O.workload_inputs(w, B)

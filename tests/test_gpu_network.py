@@ -3,7 +3,7 @@
 
 Parity per workload (the five benchmark configurations, seeded weights and
 boards): max-abs on logits and values against the blas restatement (the
-north-star bar is 1e-4), maxErr, the gap to the double-precision pass next to
+parity bar is 1e-4), maxErr, the gap to the double-precision pass next to
 the CPU backends' own gap (tests/test_cuda.cpp:804-849), and argmax agreement
 over legal moves (>= 99.9%). Full-size batches are checked through
 properties: batch independence and repeatability, bit for bit.

@@ -1,5 +1,5 @@
 """Pins the oracle (the CPU restatement of the reference's inference pass)
-before it is trusted as the checker:
+before results are checked against it:
 - known answers the reference's own tests hold (splitmix64, encode planes,
   symmetry images, im2col, the conv and BN hand examples, the gemm beta-0
   example);
