@@ -268,7 +268,9 @@ int azh_evaluate_positions(azh_runner* r, const azh_positions* pos, int B, float
  * pinned) are allocated on its first positions call. */
 int azh_begin_positions(azh_runner* r, int slot, int B, const azh_positions* pos, azh_done_fn done, void* user);
 /* The outputs of the slot's last azh_begin_positions (NULL before its first):
- * logits mapped back from each position's symmetry, priors, legal. */
+ * logits mapped back from each position's symmetry, priors, legal. The
+ * positions form of BatchRunner::logits (include/azgo/inference_hub.hpp:46-52),
+ * carrying what Mcts::expand builds from the logits (src/mcts.cpp:152-183). */
 const float* azh_slot_position_logits(const azh_runner* r, int slot);
 const float* azh_slot_priors(const azh_runner* r, int slot);
 const uint8_t* azh_slot_legal(const azh_runner* r, int slot);
@@ -335,9 +337,10 @@ int azh_time_round_trips(azh_runner* r, int slot, int B, int iters, float* ms);
  * the passes in flight are drained and the error is returned. */
 int azh_time_pipelined(azh_runner* r, int B, int passes, float* ms);
 
-/* azh_time_pipelined for the positions path: every slot kept full through
- * azh_begin_positions on the same positions `pos` (B of them; host copies of
- * stone bytes in, logits, priors, legal actions and values out). */
+/* azh_time_pipelined for the positions path (measureGpuPipelined's loop,
+ * apps/bench.cpp:227-279): every slot kept full through azh_begin_positions
+ * on the same positions `pos` (B of them; host copies of stone bytes in,
+ * logits, priors, legal actions and values out). */
 int azh_time_pipelined_positions(azh_runner* r, const azh_positions* pos, int B, int passes, float* ms);
 
 /* ---------------------------------------------------------------- kernel probes (tests) */
