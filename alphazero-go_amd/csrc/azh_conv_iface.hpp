@@ -57,7 +57,8 @@ inline constexpr bool operator==(const ConvTiling& a, const ConvTiling& b) {
 // The workgroup shapes the convolution is built for, in the order a probe
 // indexes them. Each is compiled for every supported board size.
 constexpr ConvTiling kConvTilings[] = {{2, 2, 2, 12}, {1, 4, 1, 0}, {1, 2, 1, 0}, {1, 1, 1, 0}, {1, 8, 1, 0},
-                                       {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1}};
+                                       {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1},
+                                       {1, 1, 3, 1}};
 constexpr int kConvTilingCount = sizeof kConvTilings / sizeof kConvTilings[0];
 
 // Trunk activations (every convolution's output, the residual input and the

@@ -259,10 +259,8 @@ long convWorkgroups(ConvTiling t, int cout, int B, int boardSize) {
 }
 
 ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
-    // From a sweep of every shape over boards 5, 9, 13, 19, 32 to 256
-    // channels and batches of 1 to 512 on the MI355X (256 CUs); the rule
-    // below is within 0.3% of the best shape on average over those points
-    // for boards 5 to 13, 3% for 19x19.
+    // From sweeps of every shape over boards 5, 9, 13, 19, 32 to 256
+    // channels and batches of 1 to 512 on the MI355X (256 CUs).
     // - Whole-board shapes: a workgroup is one board and 64 output channels
     //   (4 waves of 16; 32 or 16 channels with fewer blocks), two resident
     //   per CU (256 registers per lane, 56 KB of LDS each), one hiding the
@@ -280,12 +278,25 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     const int coBlocks = ceilDiv(cout, kCoBlock);
     const int groups = ceilDiv(boardSize * boardSize, 16);
     const long tiles = (long)B * coBlocks * groups;
+    const long cus = deviceCUs();
+    // The smallest layers: 3 waves of one column group each, while its
+    // workgroups fill at most half the CUs (a second pass in flight then
+    // still finds free CUs). Against the 4-wave shape they replace, per
+    // pass: 19x19 10x128 at batch 1 and 2 5-6% shorter alone and 8-12% more
+    // positions/s with two passes in flight; 19x19 20x256 at batch 1 7% and
+    // 23%; 9x9 6x64 at 8 and 16 boards 4% and 5%. Past half the CUs a pass
+    // alone still gains 3-8% with this shape or with 6-wave ones, but two
+    // passes in flight lose up to 20%, so the 4- and 8-wave shapes stay.
+    {
+        const ConvTiling t{1, 1, 3, 1};
+        if (2 * convWorkgroups(t, cout, B, boardSize) <= cus) return t;
+    }
     if (boardSize >= 19) {
         // One round of one 4-wave workgroup per CU, or nearly: the
         // whole-board shape (128 boards at 128 channels: 104.8 us per layer
         // against 114 for the next best).
         const long wholeWorkgroups = (long)B * ceilDiv(coBlocks, 4);
-        if (coBlocks >= 4 && wholeWorkgroups <= deviceCUs() && 10 * wholeWorkgroups >= 9L * deviceCUs())
+        if (coBlocks >= 4 && wholeWorkgroups <= cus && 10 * wholeWorkgroups >= 9L * cus)
             return {1, 4, 1, 0};
         if (tiles >= 40000) {
             if (coBlocks >= 4) return {1, 4, 1, 0};
@@ -298,7 +309,7 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
         if (tiles >= 1024) return {1, 1, 8, 1};
         return {1, 1, 4, 1};
     }
-    const long need = (long)(groups <= 2 ? 2 : 3) * deviceCUs();   // waves
+    const long need = (long)(groups <= 2 ? 2 : 3) * cus;   // waves
     for (const ConvTiling t : {ConvTiling{1, 4, 1, 0}, ConvTiling{1, 2, 1, 0}, ConvTiling{1, 1, 1, 0}}) {
         if (t.wavesCo > 1 && coBlocks < t.wavesCo) continue;
         const long waves = (long)B * ceilDiv(coBlocks, t.wavesCo) * t.wavesCo;

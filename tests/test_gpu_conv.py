@@ -16,10 +16,13 @@ What the tests pin:
 import numpy as np
 import pytest
 
+import build
 import oracle as O
 from _util import (U, bitwise_equal, conv_exact_and_bound, epilogue_f32, oracle_conv_raw)
 
 pytestmark = pytest.mark.gpu
+
+TILINGS = build.conv_tiling_count()   # the workgroup shapes the kernel is built for
 
 SHAPES = [  # (n, cin, cout, B): stem and tower shapes of the five workloads, plus ragged ones
     (5, 18, 32, 3), (5, 32, 32, 8), (9, 18, 64, 2), (9, 64, 64, 5), (19, 18, 128, 2), (19, 128, 128, 3),
@@ -69,7 +72,7 @@ def test_tilings_bitwise_identical(hip, n, cin, cout):
     x = _rand(rng, 3, cin, n * n)
     w = _rand(rng, cout, cin * 9, lo=-0.1, hi=0.1)
     s, h = _rand(rng, cout), _rand(rng, cout)
-    outs = [hip.probe_conv3x3(x, w, s, h, relu=True, tiling=t) for t in range(10)]
+    outs = [hip.probe_conv3x3(x, w, s, h, relu=True, tiling=t) for t in range(TILINGS)]
     for o in outs[1:]:
         assert bitwise_equal(o, outs[0])
 
@@ -86,7 +89,7 @@ def test_stem_last_chunk_every_tiling(hip, cin):
     x = _rand(rng, B, cin, n * n)
     w = (rng.standard_normal((cout, cin * 9)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
     ones, zeros = np.ones(cout, np.float32), np.zeros(cout, np.float32)
-    outs = [hip.probe_conv3x3(x, w, ones, zeros, relu=False, tiling=t) for t in range(10)]
+    outs = [hip.probe_conv3x3(x, w, ones, zeros, relu=False, tiling=t) for t in range(TILINGS)]
     for o in outs[1:]:
         assert bitwise_equal(o, outs[0])
     exact, mag = conv_exact_and_bound(x, w)
