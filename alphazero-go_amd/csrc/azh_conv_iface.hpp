@@ -45,7 +45,10 @@ struct ConvTiling {
     int waves() const { return wavesCo * wavesPg; }
     int coTile() const { return 16 * coPerWave * wavesCo; }
 };
-ConvTiling chooseConvTiling(int cout, int B, int boardSize);
+// alone: no other pass is in flight on the device (the runner's other slots
+// idle), which admits the shapes that are fastest for one pass but slower
+// for two side by side.
+ConvTiling chooseConvTiling(int cout, int B, int boardSize, bool alone = false);
 // The stem's shape in a pass whose tower runs `tower` over B boards in all
 // (both halves of a split pass, which run at once).
 ConvTiling chooseStemTiling(ConvTiling tower, int cout, int B);
@@ -58,7 +61,7 @@ inline constexpr bool operator==(const ConvTiling& a, const ConvTiling& b) {
 // indexes them. Each is compiled for every supported board size.
 constexpr ConvTiling kConvTilings[] = {{2, 2, 2, 12}, {1, 4, 1, 0}, {1, 2, 1, 0}, {1, 1, 1, 0}, {1, 8, 1, 0},
                                        {1, 2, 2, 12}, {1, 1, 4, 6}, {1, 1, 4, 2}, {1, 1, 4, 1}, {1, 1, 8, 1},
-                                       {1, 1, 3, 1}};
+                                       {1, 1, 3, 1}, {1, 1, 6, 1}, {1, 1, 6, 2}};
 constexpr int kConvTilingCount = sizeof kConvTilings / sizeof kConvTilings[0];
 
 // Trunk activations (every convolution's output, the residual input and the

@@ -258,7 +258,7 @@ long convWorkgroups(ConvTiling t, int cout, int B, int boardSize) {
     return (long)B * ceilDiv(cout, t.coTile()) * ceilDiv(groups, groupsPerWorkgroup);
 }
 
-ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
+ConvTiling chooseConvTiling(int cout, int B, int boardSize, bool alone) {
     // From sweeps of every shape over boards 5, 9, 13, 19, 32 to 256
     // channels and batches of 1 to 512 on the MI355X (256 CUs).
     // - Whole-board shapes: a workgroup is one board and 64 output channels
@@ -279,15 +279,32 @@ ConvTiling chooseConvTiling(int cout, int B, int boardSize) {
     const int groups = ceilDiv(boardSize * boardSize, 16);
     const long tiles = (long)B * coBlocks * groups;
     const long cus = deviceCUs();
-    // The smallest layers: 3 waves of one column group each, while its
-    // workgroups fill at most half the CUs (a second pass in flight then
-    // still finds free CUs). Against the 4-wave shape they replace, per
-    // pass: 19x19 10x128 at batch 1 and 2 5-6% shorter alone and 8-12% more
-    // positions/s with two passes in flight; 19x19 20x256 at batch 1 7% and
-    // 23%; 9x9 6x64 at 8 and 16 boards 4% and 5%. Past half the CUs a pass
-    // alone still gains 3-8% with this shape or with 6-wave ones, but two
-    // passes in flight lose up to 20%, so the 4- and 8-wave shapes stay.
-    {
+    // Small layers with the GPU to themselves: the shape of one block of 16
+    // channels and 3, 6 or 12 column groups per workgroup (3 waves of one
+    // group, 6 of one, 6 of two), the first whose workgroups still fit one
+    // per CU and, past the first, fill at least 70% of the CUs (a shape that
+    // leaves a third of the CUs idle loses: 19x19 at 192 channels, 6 boards,
+    // 1.56x the best). The 6-wave shapes need the board's column groups to
+    // fill their slots (all but one): on 5x5 and 9x9 boards the rest would
+    // idle. One such workgroup per CU beats the 4- and 8-wave shapes by
+    // 3-8% per layer (19x19 10x128 at batch 8: 12.95 against 13.59 us; 9x9
+    // 6x64 at 64 boards: 7.43 against 7.95) and whole passes by 2.5-8%; over
+    // boards 5-19, 32-256 channels and batches 1-192 the layer rule lands
+    // within 1.4% of the best of the 13 shapes on average (3.0% with
+    // another pass in flight, 4.3% without the three small shapes). With
+    // another pass in flight they lose up to 20% of the two passes' rate
+    // (both fill every CU), so there only the 3-wave shape is taken, while
+    // its workgroups fill at most half the CUs (19x19
+    // 10x128 at batch 1 and 2: passes 5-6% shorter, 13-14% more positions/s
+    // with two in flight; 19x19 20x256 at batch 1 7% and 21%; 9x9 6x64 at 8
+    // and 16 boards 4% and 8-13%).
+    if (alone) {
+        for (const ConvTiling t : {ConvTiling{1, 1, 3, 1}, ConvTiling{1, 1, 6, 1}, ConvTiling{1, 1, 6, 2}}) {
+            if (t.wavesPg > 3 && t.wavesPg * t.pgPerWave > groups + 1) continue;
+            const long w = convWorkgroups(t, cout, B, boardSize);
+            if (w <= cus && (t.wavesPg == 3 || 10 * w >= 7 * cus)) return t;
+        }
+    } else {
         const ConvTiling t{1, 1, 3, 1};
         if (2 * convWorkgroups(t, cout, B, boardSize) <= cus) return t;
     }

@@ -974,8 +974,19 @@ struct azh_runner {
 
     // The residual tower over slot s's whole batch on one stream, every
     // launch over all B boards (the tower kernel as timed on its own).
-    int launchTower(Slot& s, int B, hipStream_t stream, int blocksToRun) {
-        return launchTowerOn(s.dX, s.dMid, B, azh::chooseConvTiling(shape.F, B, shape.n), stream, blocksToRun);
+    int launchTower(Slot& s, int B, hipStream_t stream, int blocksToRun, bool alone) {
+        return launchTowerOn(s.dX, s.dMid, B, azh::chooseConvTiling(shape.F, B, shape.n, alone), stream,
+                             blocksToRun);
+    }
+
+    // Whether no slot but `except` (null: none) has a pass in flight or a
+    // synchronous call running: a pass enqueued now has the device to
+    // itself, as far as this runner knows (the workgroup shapes then may
+    // take every CU, chooseConvTiling).
+    bool othersIdle(const Slot* except) const {
+        for (const auto& o : slots)
+            if (o.get() != except && o->claimed.load(std::memory_order_acquire)) return false;
+        return true;
     }
 
     // Where a pass over Bp boards reads and writes: the input planes
@@ -1094,7 +1105,7 @@ struct azh_runner {
     //   two slots the four chains lose (9x9 6x64, 100 boards: -4% alone,
     //   -18% with two slots; 19x19 20x256, 8 boards: +7% alone, -19% with
     //   two slots).
-    bool splitPass(int B) const {
+    bool splitPass(int B, bool alone) const {
         if (B < 2 || useSmallTower(B)) return false;
         // A layer of under 0.5 GFLOP of matrix work (3 us at the fp32 MFMA
         // peak) is bound by its launch, and a second chain's launches only
@@ -1103,7 +1114,7 @@ struct azh_runner {
         const double layerFlops = 2.0 * B * shape.A * 16.0 * azh::ceilDiv(shape.F, azh::kCoBlock) * 16.0 *
                                   azh::ceilDiv(shape.F, azh::kChunk) * 9.0;
         if (layerFlops < 0.5e9) return false;
-        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n, alone);
         const long workgroups = azh::convWorkgroups(t, shape.F, B, shape.n);
         const long cus = azh::deviceCUs();
         if (t.pgPerWave == 0) return workgroups > cus;
@@ -1116,10 +1127,11 @@ struct azh_runner {
     // the part's own batch's shape unless that is a whole-board one (a
     // 19x19 half of 120 boards at 96 channels would take the one-round
     // shape: 141.7 us per layer in halves, 122.1 with the batch's shape).
-    azh::ConvTiling partTiling(int B, int Bp) const {
-        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n);
+    azh::ConvTiling partTiling(int B, int Bp, bool alone) const {
+        const azh::ConvTiling t = azh::chooseConvTiling(shape.F, B, shape.n, alone);
         if (t.pgPerWave == 0 || Bp == B) return t;
-        const azh::ConvTiling own = azh::chooseConvTiling(shape.F, Bp, shape.n);
+        // The two halves run side by side: neither is alone.
+        const azh::ConvTiling own = azh::chooseConvTiling(shape.F, Bp, shape.n, false);
         return own.pgPerWave == 0 ? t : own;
     }
 
@@ -1128,8 +1140,8 @@ struct azh_runner {
     // two halves, the second on s.aux, forked from `stream` and joined back
     // into it.
     template <typename Part>
-    void overHalves(Slot& s, int B, hipStream_t stream, Part part) {
-        if (!splitPass(B)) {
+    void overHalves(Slot& s, int B, hipStream_t stream, bool alone, Part part) {
+        if (!splitPass(B, alone)) {
             part(0, B, stream);
             return;
         }
@@ -1142,17 +1154,18 @@ struct azh_runner {
         check(hipStreamWaitEvent(stream, s.join, 0), "hipStreamWaitEvent(join)");
     }
 
-    // The pass's kernels, on `stream`, in halves when the pass splits.
-    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads) {
+    // The pass's kernels, on `stream`, in halves when the pass splits;
+    // alone: no other pass in flight (othersIdle).
+    void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads, bool alone) {
         const bool small = useSmallTower(B);
-        overHalves(s, B, stream, [&](int b0, int Bp, hipStream_t st) {
-            launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp), st, blocksToRun, heads, small);
+        overHalves(s, B, stream, alone, [&](int b0, int Bp, hipStream_t st) {
+            launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp, alone), st, blocksToRun, heads, small);
         });
     }
 
     // The tower as the pass runs it, on slot s's staged trunk (the effective
     // time per layer within a pass).
-    void launchTowerAsPass(Slot& s, int B, int blocksToRun) {
+    void launchTowerAsPass(Slot& s, int B, int blocksToRun, bool alone) {
         if (useSmallTower(B)) {
             check(azh::launchSmallTower(s.dX, nullptr, nullptr, tower.w0, tower.stride, tower.scaleOff,
                                         tower.shiftOff, 2 * std::max(blocksToRun, 0), B, shape.n, shape.F,
@@ -1161,8 +1174,8 @@ struct azh_runner {
             return;
         }
         const size_t trunk = azh::quadFloats(1, shape.F, shape.A);
-        overHalves(s, B, s.stream, [&](int b0, int Bp, hipStream_t st) {
-            launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, partTiling(B, Bp), st, blocksToRun);
+        overHalves(s, B, s.stream, alone, [&](int b0, int Bp, hipStream_t st) {
+            launchTowerOn(s.dX + b0 * trunk, s.dMid + b0 * trunk, Bp, partTiling(B, Bp, alone), st, blocksToRun);
         });
     }
 
@@ -1172,13 +1185,15 @@ struct azh_runner {
     // least recently, after the slot's stream has finished with it.
     static constexpr size_t kGraphsPerSlot = 64;
     void enqueuePass(Slot& s, int B) {
+        const bool alone = othersIdle(&s);
         if (!graphs) {
-            launchPass(s, B, s.stream, shape.blocks, true);
+            launchPass(s, B, s.stream, shape.blocks, true, alone);
             return;
         }
-        // One graph per batch size and tower form (the small-board tower can
-        // be switched off by a test hook).
-        const int key = 2 * B + (useSmallTower(B) ? 1 : 0);
+        // One graph per batch size, workgroup-shape regime (another pass in
+        // flight or not) and tower form (the small-board tower can be
+        // switched off by a test hook).
+        const int key = 4 * B + (alone ? 2 : 0) + (useSmallTower(B) ? 1 : 0);
         auto it = s.graphs.find(key);
         if (it == s.graphs.end()) {
             if (s.graphs.size() >= kGraphsPerSlot) {
@@ -1192,7 +1207,7 @@ struct azh_runner {
             hipGraph_t g = nullptr;
             check(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             try {
-                launchPass(s, B, s.stream, shape.blocks, true);
+                launchPass(s, B, s.stream, shape.blocks, true, alone);
             } catch (...) {
                 (void)hipStreamEndCapture(s.stream, &g);
                 if (g) (void)hipGraphDestroy(g);
@@ -1685,9 +1700,10 @@ int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, f
         float* x = scratchOnCurrentDevice();
         float* mid = x + alignFloats(azh::quadFloats(B, sh.F, sh.A));
         float* act = mid + alignFloats(azh::quadFloats(B, sh.F, sh.A));
+        // Alone when none of the runner's slots has a pass in flight.
         r->launchPassPart(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B, B,
-                          azh::chooseConvTiling(sh.F, B, sh.n), static_cast<hipStream_t>(stream), sh.blocks, true,
-                          r->useSmallTower(B));
+                          azh::chooseConvTiling(sh.F, B, sh.n, r->othersIdle(nullptr)),
+                          static_cast<hipStream_t>(stream), sh.blocks, true, r->useSmallTower(B));
     });
 }
 
@@ -1907,7 +1923,8 @@ int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, i
         // The tower as the pass runs it: every block's two convolutions in
         // order, each reading the previous one's output.
         int per = 0;
-        *ms = timeOnStream(s.stream, iters, [&] { per = r->launchTower(s, B, s.stream, r->shape.blocks); });
+        const bool alone = r->othersIdle(&s);
+        *ms = timeOnStream(s.stream, iters, [&] { per = r->launchTower(s, B, s.stream, r->shape.blocks, alone); });
         *launches = iters * per;
         *layers = iters * 2 * r->shape.blocks;
     });
@@ -1920,7 +1937,8 @@ int azh_time_tower_layers(azh_runner* r, int slot, int B, int iters, float* ms, 
         r->checkBatch(B);
         const SlotClaim held = r->claimIdle(slot);
         Slot& s = held.slot;
-        *ms = timeOnStream(s.stream, iters, [&] { r->launchTowerAsPass(s, B, r->shape.blocks); });
+        const bool alone = r->othersIdle(&s);
+        *ms = timeOnStream(s.stream, iters, [&] { r->launchTowerAsPass(s, B, r->shape.blocks, alone); });
         *layers = iters * 2 * r->shape.blocks;
     });
 }
@@ -1975,12 +1993,13 @@ int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const 
         // 16-channel chunks is tried as a trunk activation (channel quads,
         // the tower kernel), any other as input planes (the stem kernel).
         // Outputs and residuals are channel quads; the probe's own arrays
-        // are planar, converted here. Tiling -1: the shape a pass of B
-        // gives that kernel.
+        // are planar, converted here. Tiling -1: the shape a pass of B alone
+        // on the device gives that kernel.
         const bool planarIn = cin % azh::kChunk != 0;
+        const azh::ConvTiling pass = azh::chooseConvTiling(cout, B, n, true);
         const azh::ConvTiling t = tiling >= 0 ? kTilings[tiling]
-                                  : planarIn  ? azh::chooseStemTiling(azh::chooseConvTiling(cout, B, n), cout, B)
-                                              : azh::chooseConvTiling(cout, B, n);
+                                  : planarIn  ? azh::chooseStemTiling(pass, cout, B)
+                                              : pass;
         const std::vector<float> xq = planarIn ? std::vector<float>() : azh::toChannelQuads(x, B, cin, (int)A);
         const std::vector<float> kq = skip ? azh::toChannelQuads(skip, B, cout, (int)A) : std::vector<float>();
         const size_t fx = planarIn ? B * cin * A : xq.size(), fy = azh::quadFloats(B, cout, (int)A);
@@ -2023,10 +2042,12 @@ int azh_time_conv3x3(int B, int n, int cin, int cout, int tiling, int iters, flo
         if (!azh::conv3x3Supported(n)) throw Error(AZH_ERR_ARGUMENT, "hip: board size not supported");
         if (tiling < -1 || tiling >= kTilingCount) throw Error(AZH_ERR_ARGUMENT, "hip: tiling index out of range");
         const bool planarIn = cin % azh::kChunk != 0;   // as azh_probe_conv3x3 chooses
-        // Tiling -1: the shape a pass of B gives that kernel.
+        // Tiling -1: the shape a pass of B alone on the device gives that
+        // kernel.
+        const azh::ConvTiling pass = azh::chooseConvTiling(cout, B, n, true);
         const azh::ConvTiling t = tiling >= 0 ? kTilings[tiling]
-                                  : planarIn  ? azh::chooseStemTiling(azh::chooseConvTiling(cout, B, n), cout, B)
-                                              : azh::chooseConvTiling(cout, B, n);
+                                  : planarIn  ? azh::chooseStemTiling(pass, cout, B)
+                                              : pass;
         requireContext();
         const size_t A = (size_t)n * n;
         std::vector<float> w((size_t)cout * cin * 9);
@@ -2106,7 +2127,7 @@ int azh_probe_trunk(azh_runner* r, const float* input, int B, int blocks, float*
         const Shape& sh = r->shape;
         check(hipMemcpyAsync(s.dIn, input, (size_t)B * sh.P * sh.A * sizeof(float), hipMemcpyHostToDevice, s.stream),
               "hipMemcpyAsync");
-        r->launchPass(s, B, s.stream, blocks, false);
+        r->launchPass(s, B, s.stream, blocks, false, r->othersIdle(&s));
         std::vector<float> tq(azh::quadFloats(B, sh.F, sh.A));
         check(hipMemcpyAsync(tq.data(), s.dX, tq.size() * sizeof(float), hipMemcpyDeviceToHost, s.stream),
               "hipMemcpyAsync");

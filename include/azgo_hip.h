@@ -348,11 +348,13 @@ int azh_time_pipelined_positions(azh_runner* r, const azh_positions* pos, int B,
 /* The pass's 3x3 convolution kernel alone (cuda_probe::convBnRelu,
  * include/azgo/cuda.hpp:123-126): x [B][cin][n*n], w [cout][cin*9],
  * y [B][cout][n*n] = relu?(scale*conv + shift (+ skip)). skip may be NULL.
- * tiling: -1 the pass's rule, else an index 0..10 forcing a workgroup shape,
+ * tiling: -1 the pass's rule (for a pass alone on the device), else an index
+ * 0..12 forcing a workgroup shape,
  * (16-channel blocks per wave, waves along channels, waves along the board's
  * 16-point column groups, groups per wave; 0 = all): 0 (2,2,2,12),
  * 1 (1,4,1,0), 2 (1,2,1,0), 3 (1,1,1,0), 4 (1,8,1,0), 5 (1,2,2,12),
- * 6 (1,1,4,6), 7 (1,1,4,2), 8 (1,1,4,1), 9 (1,1,8,1), 10 (1,1,3,1). */
+ * 6 (1,1,4,6), 7 (1,1,4,2), 8 (1,1,4,1), 9 (1,1,8,1), 10 (1,1,3,1),
+ * 11 (1,1,6,1), 12 (1,1,6,2). */
 int azh_probe_conv3x3(const float* x, const float* w, const float* scale, const float* shift, const float* skip,
                       int relu, int B, int n, int cin, int cout, int tiling, float* y);
 

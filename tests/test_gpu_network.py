@@ -297,6 +297,40 @@ def test_input_plane_counts_parity(hip, history, B):
     assert bitwise_equal(alone[0][0], got[0][B - 1]) and bitwise_equal(alone[1][0], got[1][B - 1])
 
 
+@pytest.mark.parametrize("tag,B", [(4, 4), (4, 8), (4, 16), (2, 48), (2, 64), (5, 8)])
+def test_alone_and_shared_shapes_same_bits(hip, tag, B):
+    """A pass enqueued while the runner's other slot is idle takes the
+    workgroup shapes fastest for one pass (one workgroup per CU); with a pass
+    in flight on the other slot, the shapes that share the GPU better. The
+    shape decides only which workgroup computes an output: the bits are the
+    same either way, in both slots."""
+    w = O.WORKLOADS[tag]
+    net = O.random_network(w.cfg, 620 + tag)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B, slots=2) as r:
+        alone = r.infer(inp)   # slot 0, slot 1 idle
+        for slot in (0, 1):
+            r.input(slot)[:B] = inp
+        done = [threading.Event(), threading.Event()]
+        errors = []
+
+        def cb(slot, err):
+            if err:
+                errors.append(err)
+            done[slot].set()
+
+        hip.set_copy_out_delay(200000)   # each pass holds its slot for 0.2 s
+        try:
+            r.begin(1, B, cb)   # slot 0 idle: the shapes for one pass
+            r.begin(0, B, cb)   # slot 1 busy: the shapes for two
+            assert done[0].wait(60) and done[1].wait(60)
+        finally:
+            hip.set_copy_out_delay(0)
+        assert not errors, errors
+        for slot in (0, 1):
+            assert bitwise_equal(r.logits(slot, B), alone[0]) and bitwise_equal(r.values(slot, B), alone[1]), slot
+
+
 def test_repeatable_and_graph_equals_eager(hip):
     w = O.WORKLOADS[2]
     net = O.random_network(w.cfg, 604)
