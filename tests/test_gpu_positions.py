@@ -317,3 +317,23 @@ def test_positions_kept_full_and_failure(hip):
         assert r.time_pipelined_positions(B, 2, stones, to_move, plies, sym, seen) > 0
         for a, b in zip(r.position_outputs(0, B), want):
             assert a.tobytes() == b.tobytes()
+
+
+def test_begin_positions_defaults(hip):
+    """No plies (all H present), no symmetry and no superko lists, one
+    position and a full batch: the asynchronous pass equals the synchronous
+    one bit for bit."""
+    import threading
+    net = calibrated_network("1")
+    n, H = 5, net.cfg.history
+    g = np.random.default_rng(12)
+    with hip.Runner(to_hip_cfg(hip, net.cfg), net.tensors(), 16, 1) as r:
+        for B in (1, 16):
+            stones = g.integers(0, 3, (B, H, n * n)).astype(np.uint8)
+            to_move = g.integers(1, 3, B).astype(np.uint8)
+            want = r.evaluate_positions(stones, to_move)
+            ev = threading.Event()
+            r.begin_positions(0, lambda s, e: ev.set(), stones, to_move)
+            assert ev.wait(60)
+            for a, b in zip(r.position_outputs(0, B), want):
+                assert a.tobytes() == b.tobytes()
