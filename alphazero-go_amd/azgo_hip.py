@@ -107,6 +107,9 @@ def load():
             "azh_time_pipelined_positions": ([vp, P(Positions), C.c_int, C.c_int, f32], C.c_int),
             "azh_set_graphs": ([vp, C.c_int], C.c_int),
             "azh_set_small_tower": ([vp, C.c_int], C.c_int),
+            "azh_set_resident_tower": ([vp, C.c_int], C.c_int),
+            "azh_time_resident_tower": ([vp, C.c_int, C.c_int, C.c_int, C.c_int, f32], C.c_int),
+            "azh_pass_form": ([vp, C.c_int, C.c_int, P(C.c_int)], C.c_int),
             "azh_stage": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_enqueue": ([vp, C.c_int, C.c_int], C.c_int),
             "azh_synchronize": ([vp, C.c_int], C.c_int),
@@ -400,6 +403,11 @@ class Runner:
     def set_small_tower(self, enabled):
         _check(self.lib.azh_set_small_tower(self.h, int(enabled)))
 
+    def set_resident_tower(self, mode):
+        """0: per-layer launches; 1: the board-resident tower where the batch
+        fills its rounds of CUs (default); 2: wherever the network allows it."""
+        _check(self.lib.azh_set_resident_tower(self.h, int(mode)))
+
     # ---- slot staging (the hub's view)
     def input(self, slot):
         p = self.lib.azh_slot_input(self.h, slot)
@@ -460,6 +468,22 @@ class Runner:
         ms, layers = C.c_float(), C.c_int()
         _check(self.lib.azh_time_tower_layers(self.h, slot, B, iters, C.byref(ms), C.byref(layers)))
         return ms.value, layers.value
+
+    def time_resident_tower(self, slot, B, iters, stem=True):
+        """Total ms of `iters` board-resident launches over B boards (the stem
+        first when asked, as a pass runs it)."""
+        ms = C.c_float()
+        _check(self.lib.azh_time_resident_tower(self.h, slot, B, iters, int(stem), C.byref(ms)))
+        return ms.value
+
+    # azh_pass_form's mask bits
+    FORM_SMALL, FORM_RESIDENT, FORM_SPLIT = 1, 2, 4
+
+    def pass_form(self, B, alone=True):
+        """How a pass of B runs: a mask of FORM_SMALL, FORM_RESIDENT, FORM_SPLIT."""
+        form = C.c_int()
+        _check(self.lib.azh_pass_form(self.h, B, int(alone), C.byref(form)))
+        return form.value
 
     def time_round_trips(self, slot, B, iters):
         ms = C.c_float()

@@ -23,6 +23,7 @@ SOURCES = ["azh_kernels.hip", "azh_positions.hip", "azh_runtime.hip", "azh_small
 CONV_INST = "azh_conv_inst.hip"
 CONV_HEADERS = ["azh_conv.hpp", "azh_conv_iface.hpp", "azh_stem.hpp"]
 BOARD_SIZES = (5, 9, 13, 19)   # conv3x3Supported
+RESIDENT_BOARD_SIZES = (19,)   # residentTowerSupported
 HEADERS = CONV_HEADERS + ["azh_kernels.hpp", "azh_heads.hpp", os.path.join("..", "..", "include", "azgo_hip.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -75,6 +76,8 @@ def build(verbose=False, jobs=None, incremental=False):
     for n in BOARD_SIZES:
         for t in range(conv_tiling_count()):
             units.append((CONV_INST, f"azh_conv_{n}_{t}.o", [f"-DAZH_CONV_N={n}", f"-DAZH_CONV_TILING={t}"]))
+    for n in RESIDENT_BOARD_SIZES:
+        units.append((CONV_INST, f"azh_resident_{n}.o", [f"-DAZH_CONV_N={n}", "-DAZH_RESIDENT_TOWER"]))
 
     deps = [os.path.join(CSRC, f) for f in SOURCES + [CONV_INST] + HEADERS] + [os.path.abspath(__file__)]
     newest = max(os.path.getmtime(f) for f in deps)

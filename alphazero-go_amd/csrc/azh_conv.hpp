@@ -377,17 +377,17 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
     writeOutputs<N, 1, PPW>(acc, ep, skip != nullptr, y, b, cout, cb0, pg0, k, n16, relu);
 }
 
-// A workgroup computes one board's output channels [co tile] at column
-// groups [pixel tile]: WCO x WPG waves, wave (c, g) owning COW blocks of 16
-// channels and PPW column groups (PPW = 0: all of them). PLANAR: x is the
+// A workgroup computes board b's output channels [co tile ct] at column
+// groups [pixel tile pt]: WCO x WPG waves, wave (c, g) owning COW blocks of
+// 16 channels and PPW column groups (PPW = 0: all of them). PLANAR: x is the
 // network's input planes [B][cin][A] (the stem), read a channel at a time;
 // otherwise x is a trunk activation in channel quads, read a quad at a time.
-// Either way input channels past cin are read as zeros.
+// Either way input channels past cin are read as zeros. tid: threadIdx.x.
 template <int N, int COW, int WCO, int WPG, int PPW0, bool PLANAR>
 __device__ __forceinline__ void conv3x3Body(f4* lds, const float* __restrict__ x, const f4* __restrict__ wp,
                                             const float* __restrict__ scale, const float* __restrict__ shift,
-                                            const float* skip, float* y, int cin, int cout, int nq, int coTiles,
-                                            int pixTiles, int relu) {
+                                            const float* skip, float* y, int cin, int cout, int nq, int b, int ct,
+                                            int pt, int relu, int tid) {
     using G = Geo<N>;
     constexpr int PPW = PPW0 == 0 ? G::NPG : PPW0;
     constexpr int WAVES = WCO * WPG;
@@ -401,15 +401,7 @@ __device__ __forceinline__ void conv3x3Body(f4* lds, const float* __restrict__ x
     constexpr int ITEMS = 4 * ROWS * N;   // (channel group, point) pairs per chunk, at most
     constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Workgroups are dealt to the 8 XCDs round-robin; renumber so that the
-    // co tiles of one board run on the same XCD and share its L2.
-    const int total = gridDim.x;
-    const int wg = blockIdx.x;
-    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
-    const int tilesPerBoard = coTiles * pixTiles;
-    const int b = logical / tilesPerBoard, tile = logical % tilesPerBoard;
-    const int ct = tile / pixTiles, pt = tile % pixTiles;
+    const int lane = tid & 63, wave = tid >> 6;
     const int cb0 = (ct * WCO + wave / WPG) * COW;
     // This wave's first column group (a constant 0 when every wave covers the board).
     const int pg0 = PPW0 == 0 ? 0 : (pt * WPG + wave % WPG) * PPW;
@@ -570,23 +562,20 @@ __device__ __forceinline__ void conv3x3Body(f4* lds, const float* __restrict__ x
 // units idle meanwhile), and the stem's last-chunk weights and BN factors
 // are fetched before the first MFMA (half the accumulators leave the
 // registers for them). The MFMA sequence per output, and so every bit, is
-// the general body's. lds: two chunk buffers of the general body's layout.
+// the general body's. lds: two chunk buffers of the general body's layout;
+// the workgroup computes board b's co tile ct; tid: threadIdx.x.
 template <int N, int COW, int WCO>
 __device__ __forceinline__ void conv3x3StemWhole(f4* lds, const float* __restrict__ x, const f4* __restrict__ wp,
                                                  const float* __restrict__ scale, const float* __restrict__ shift,
-                                                 float* y, int cin, int cout, int nq, int coTiles, int relu) {
+                                                 float* y, int cin, int cout, int nq, int b, int ct, int relu,
+                                                 int tid) {
     using G = Geo<N>;
     constexpr int THREADS = WCO * 64;
     constexpr int HALF = (G::NPG + 1) / 2;   // column groups per half (the second may hold one fewer)
     constexpr int ITEMS = 4 * G::A;          // (channel group, point) pairs per chunk
     constexpr int PER = (ITEMS + THREADS - 1) / THREADS;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Co tiles of one board on one XCD (as the general body numbers them).
-    const int total = gridDim.x;
-    const int wg = blockIdx.x;
-    const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;
-    const int b = logical / coTiles, ct = logical % coTiles;
+    const int lane = tid & 63, wave = tid >> 6;
     const int cb0 = (ct * WCO + wave) * COW;
     const int k = lane >> 4, n16 = lane & 15;
 
@@ -720,21 +709,82 @@ __device__ __forceinline__ void conv3x3StemWhole(f4* lds, const float* __restric
                                                   pixTiles, relu);                                         \
         } else {                                                                                           \
             __shared__ f4 lds[2 * Geo<N>::BUF];                                                            \
+            /* Workgroups are dealt to the 8 XCDs round-robin; renumbered so */                            \
+            /* that the tiles of one board run on the same XCD (one L2). */                                \
+            const int total = gridDim.x, wg = blockIdx.x;                                                  \
+            const int logical = (total % 8 == 0) ? (wg % 8) * (total / 8) + wg / 8 : wg;                   \
+            const int b = logical / (coTiles * pixTiles), tile = logical % (coTiles * pixTiles);           \
+            const int ct = tile / pixTiles, pt = tile % pixTiles;                                          \
             if constexpr (PLANAR && PPW == 0 && WPG == 1) {                                                \
                 if (nq <= 2 && !skip) {                                                                    \
-                    conv3x3StemWhole<N, COW, WCO>(lds, x, wp, scale, shift, y, cin, cout, nq, coTiles, relu); \
+                    conv3x3StemWhole<N, COW, WCO>(lds, x, wp, scale, shift, y, cin, cout, nq, b, ct, relu,     \
+                                                  threadIdx.x);                                    \
                     return;                                                                                \
                 }                                                                                          \
             }                                                                                              \
-            conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(lds, x, wp, scale, shift, skip, y, cin, cout, nq,     \
-                                                       coTiles, pixTiles, relu);                           \
+            conv3x3Body<N, COW, WCO, WPG, PPW, PLANAR>(lds, x, wp, scale, shift, skip, y, cin, cout, nq, b,  \
+                                                       ct, pt, relu, threadIdx.x);                         \
         }                                                                                                  \
     }
 AZH_CONV_KERNEL(conv3x3Tower, false)
 AZH_CONV_KERNEL(conv3x3Stem, true)
 #undef AZH_CONV_KERNEL
 
+// threadIdx.x as a value the compiler cannot see through: the bodies'
+// per-lane addresses are then computed again for each layer instead of
+// hoisted out of the loops and held across them (which spills).
+__device__ __forceinline__ int opaqueThreadIdx() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// The board-resident tower: one workgroup of 8 waves holds a board for the
+// stem (when t.in is set) and every layer of the tower, with a workgroup
+// barrier between layers in place of a kernel boundary (a board's layer
+// reads only that board's previous layer, which the same workgroup wrote).
+// Each layer is the general body on the whole board at 128 output channels
+// per workgroup (wave w: channels 16w..16w+15), so every output has the
+// per-layer launches' MFMA sequence and bits. The workgroup takes boards
+// blockIdx.x, + gridDim.x, ...; the layers' activations go through global
+// memory (x and mid as the per-layer launches use them), and the
+// barrier's workgroup-scope fence orders a layer's stores before the next
+// layer's loads. STEM: the launch runs the stem first (t.in set); a kernel
+// of its own, apart from the tower alone, so that profiles tell them apart.
+template <int N, bool STEM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void convTowerResident(
+    ResidentTower t) {
+    __shared__ f4 lds[2 * Geo<N>::BUF];
+    const int nq = (t.F + kChunk - 1) / kChunk;
+    for (int b = blockIdx.x; b < t.B; b += gridDim.x) {
+        if constexpr (STEM) {
+            conv3x3StemWhole<N, 1, 8>(lds, t.in, reinterpret_cast<const f4*>(t.stemW), t.stemScale, t.stemShift, t.x,
+                                      t.P, t.F, (t.P + kChunk - 1) / kChunk, b, 0, 1, opaqueThreadIdx());
+            __syncthreads();
+        }
+        for (int l = 0; l < t.layers; ++l) {
+            const float* w = t.w0 + (size_t)l * t.stride;
+            // Even layers: a block's first convolution, x -> mid; odd: its
+            // second, mid -> x with x as the residual (in place).
+            const bool second = (l & 1) != 0;
+            conv3x3Body<N, 1, 8, 1, 0, false>(lds, second ? t.mid : t.x, reinterpret_cast<const f4*>(w),
+                                               w + t.scaleOff, w + t.shiftOff, second ? t.x : nullptr,
+                                               second ? t.x : t.mid, t.F, t.F, nq, b, 0, 0, 1, opaqueThreadIdx());
+            __syncthreads();
+        }
+    }
+}
+
 } // namespace
+
+template <int N>
+hipError_t launchResidentTowerT(const ResidentTower& t, int workgroups, hipStream_t stream) {
+    if (t.in)
+        hipLaunchKernelGGL((convTowerResident<N, true>), dim3(workgroups), dim3(512), 0, stream, t);
+    else
+        hipLaunchKernelGGL((convTowerResident<N, false>), dim3(workgroups), dim3(512), 0, stream, t);
+    return hipGetLastError();
+}
 
 template <int N, int COW, int WCO, int WPG, int PPW>
 hipError_t launchConvT(const float* x, const float* wp, const float* scale, const float* shift, const float* skip,

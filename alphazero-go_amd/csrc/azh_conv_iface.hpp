@@ -96,6 +96,30 @@ hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scal
                          ConvTiling tiling, hipStream_t stream);
 bool conv3x3Supported(int boardSize);
 
+// The stem and the residual tower in one launch, each board resident in one
+// workgroup of 8 waves (128 output channels) from its first layer to its
+// last: the per-layer launches' arithmetic without their kernel boundaries.
+// For networks of 113-128 channels (every wave a block of 16) and stems of
+// up to 32 planes, on the board sizes residentTowerSupported names.
+struct ResidentTower {
+    const float* in;   // the network's input planes [B][P][A]; null: no stem (x holds the tower's input)
+    const float *stemW, *stemScale, *stemShift;   // the stem's packed weights and folded BN
+    int P;
+    float* x;     // the trunk (channel quads), in place
+    float* mid;   // the blocks' middle activations
+    // Tower layer l (conv1, conv2 of each block in turn): packed weights at
+    // w0 + l * stride, its BN scale and shift scaleOff and shiftOff floats
+    // after them.
+    const float* w0;
+    size_t stride, scaleOff, shiftOff;
+    int layers, B, F;
+};
+bool residentTowerSupported(int boardSize, int F, int P);
+// workgroups: at most B; each takes every workgroups-th board.
+hipError_t launchResidentTower(const ResidentTower& t, int boardSize, int workgroups, hipStream_t stream);
+template <int N>
+hipError_t launchResidentTowerT(const ResidentTower& t, int workgroups, hipStream_t stream);
+
 // y = relu?(scale * acc + shift (+ skip)), each operation rounded on its own.
 __device__ inline float epilogue(float acc, float s, float h, bool addSkip, float skipv, bool relu) {
     float v = __fadd_rn(__fmul_rn(s, acc), h);

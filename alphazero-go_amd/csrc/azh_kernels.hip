@@ -349,6 +349,20 @@ ConvTiling chooseStemTiling(ConvTiling tower, int cout, int B) {
     return tower;
 }
 
+bool residentTowerSupported(int boardSize, int F, int P) {
+    // Built for 19x19 (azh_conv_inst.hip); 8 waves of 16 channels, all but
+    // the last block of them full; the stem's planes in two chunks.
+    return boardSize == 19 && F > 112 && F <= 128 && P >= 1 && P <= 2 * kChunk;
+}
+
+hipError_t launchResidentTower(const ResidentTower& t, int boardSize, int workgroups, hipStream_t stream) {
+    if (!residentTowerSupported(boardSize, t.F, t.in ? t.P : 1) || t.layers < 0 || workgroups < 1 ||
+        workgroups > t.B || !t.x || !t.mid || (t.layers > 0 && !t.w0) ||
+        (t.in && (!t.stemW || !t.stemScale || !t.stemShift)))
+        return hipErrorInvalidValue;
+    return launchResidentTowerT<19>(t, workgroups, stream);
+}
+
 hipError_t launchConv3x3(const float* x, const float* wPacked, const float* scale, const float* shift,
                          const float* skip, float* y, int B, int n, int cin, int cout, bool relu, bool planarInput,
                          ConvTiling t, hipStream_t stream) {

@@ -936,6 +936,10 @@ struct azh_runner {
     // allowed (a test hook turns it off), and the tower convolutions' place
     // in the weight arena (one fixed stride; `tower.ok` once checked).
     bool smallTower = true;
+    // The board-resident tower (azh::launchResidentTower): 0 never, 1 for a
+    // pass alone on the device whose batch fills its rounds of CUs
+    // (useResidentTower), 2 wherever the network allows it (a test hook).
+    int residentTower = 1;
     struct TowerLayout {
         bool ok = false;
         const float* w0 = nullptr;
@@ -1086,6 +1090,53 @@ struct azh_runner {
         return false;
     }
 
+    // Whether a pass of B runs its stem and tower as one board-resident
+    // launch (alone: no other pass in flight, othersIdle). A board's tower
+    // takes the same time on its CU whatever the batch (19x19 10x128: 3.90
+    // ms per pass up to 256 boards), so a round of workgroups part-filled
+    // idles CUs for all of it, while the per-layer launches shrink with the
+    // batch: taken when the rounds are at least 97% full (per pass at 256
+    // boards 3.90 against 3.97 ms, at 512 7.76 against 7.79; at 240 3.90
+    // against 3.87). Not with another pass in flight: its workgroups hold
+    // every CU's registers for a whole tower, so the other pass's kernels
+    // (heads included) wait for them (two slots kept full: 63.7k against
+    // 64.7k positions/s).
+    bool useResidentTower(int B, bool alone) const {
+        const Shape& sh = shape;
+        if (residentTower == 0 || (!tower.ok && sh.blocks > 0) || B < 1 ||
+            !azh::residentTowerSupported(sh.n, sh.F, sh.P))
+            return false;
+        if (residentTower == 2) return true;
+        const long cus = azh::deviceCUs();
+        const long rounds = (B + cus - 1) / cus;
+        return alone && 100L * B >= 97L * rounds * cus;
+    }
+
+    // The stem (when asked) and the tower's first `blocksToRun` blocks over
+    // io's Bp boards as one board-resident launch.
+    void launchResident(const PassBuffers& io, int Bp, hipStream_t stream, int blocksToRun, bool stem) {
+        const Shape& sh = shape;
+        azh::ResidentTower t{};
+        if (stem) {
+            t.in = io.in;
+            t.stemW = weights.stem.w;
+            t.stemScale = weights.stem.scale;
+            t.stemShift = weights.stem.shift;
+            t.P = sh.P;
+        }
+        t.x = io.x;
+        t.mid = io.mid;
+        t.w0 = tower.w0;
+        t.stride = tower.stride;
+        t.scaleOff = tower.scaleOff;
+        t.shiftOff = tower.shiftOff;
+        t.layers = 2 * std::max(blocksToRun, 0);
+        t.B = Bp;
+        t.F = sh.F;
+        const int workgroups = (int)std::min<long>(Bp, azh::deviceCUs());
+        check(azh::launchResidentTower(t, sh.n, workgroups, stream), "board-resident tower");
+    }
+
     // Whether a pass of B runs as two half-batch chains on two streams.
     // - Whole-board shapes with more than one round of workgroups (more than
     //   one per CU): two independent halves drift apart, so one half's
@@ -1106,7 +1157,7 @@ struct azh_runner {
     //   -18% with two slots; 19x19 20x256, 8 boards: +7% alone, -19% with
     //   two slots).
     bool splitPass(int B, bool alone) const {
-        if (B < 2 || useSmallTower(B)) return false;
+        if (B < 2 || useSmallTower(B) || useResidentTower(B, alone)) return false;
         // A layer of under 0.5 GFLOP of matrix work (3 us at the fp32 MFMA
         // peak) is bound by its launch, and a second chain's launches only
         // add to it (5x5 4x32, 300 boards: 0.14 GFLOP per layer, 5.4 ->
@@ -1157,6 +1208,15 @@ struct azh_runner {
     // The pass's kernels, on `stream`, in halves when the pass splits;
     // alone: no other pass in flight (othersIdle).
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads, bool alone) {
+        if (useResidentTower(B, alone)) {
+            const PassBuffers io = slotBuffers(s, 0);
+            launchResident(io, B, stream, blocksToRun, true);
+            if (heads)
+                check(azh::launchHeads(io.x, weights.heads, io.act, io.logits, io.values, io.own, B, shape.n, shape.F,
+                                       shape.V, stream),
+                      "heads");
+            return;
+        }
         const bool small = useSmallTower(B);
         overHalves(s, B, stream, alone, [&](int b0, int Bp, hipStream_t st) {
             launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp, alone), st, blocksToRun, heads, small);
@@ -1166,6 +1226,10 @@ struct azh_runner {
     // The tower as the pass runs it, on slot s's staged trunk (the effective
     // time per layer within a pass).
     void launchTowerAsPass(Slot& s, int B, int blocksToRun, bool alone) {
+        if (useResidentTower(B, alone)) {
+            launchResident(slotBuffers(s, 0), B, s.stream, blocksToRun, false);
+            return;
+        }
         if (useSmallTower(B)) {
             check(azh::launchSmallTower(s.dX, nullptr, nullptr, tower.w0, tower.stride, tower.scaleOff,
                                         tower.shiftOff, 2 * std::max(blocksToRun, 0), B, shape.n, shape.F,
@@ -1191,9 +1255,9 @@ struct azh_runner {
             return;
         }
         // One graph per batch size, workgroup-shape regime (another pass in
-        // flight or not) and tower form (the small-board tower can be
-        // switched off by a test hook).
-        const int key = 4 * B + (alone ? 2 : 0) + (useSmallTower(B) ? 1 : 0);
+        // flight or not) and tower form (test hooks switch the small-board
+        // and the board-resident towers).
+        const int key = 8 * B + (useResidentTower(B, alone) ? 4 : 0) + (alone ? 2 : 0) + (useSmallTower(B) ? 1 : 0);
         auto it = s.graphs.find(key);
         if (it == s.graphs.end()) {
             if (s.graphs.size() >= kGraphsPerSlot) {
@@ -1860,6 +1924,14 @@ int azh_set_small_tower(azh_runner* r, int enabled) {
     });
 }
 
+int azh_set_resident_tower(azh_runner* r, int mode) {
+    return guarded([&] {
+        if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
+        if (mode < 0 || mode > 2) throw Error(AZH_ERR_ARGUMENT, "hip: resident tower mode must be 0, 1 or 2");
+        r->residentTower = mode;
+    });
+}
+
 int azh_stage(azh_runner* r, int slot, int B) {
     return guarded([&] {
         if (!r) throw Error(AZH_ERR_ARGUMENT, "hip: no runner");
@@ -1940,6 +2012,29 @@ int azh_time_tower_layers(azh_runner* r, int slot, int B, int iters, float* ms, 
         const bool alone = r->othersIdle(&s);
         *ms = timeOnStream(s.stream, iters, [&] { r->launchTowerAsPass(s, B, r->shape.blocks, alone); });
         *layers = iters * 2 * r->shape.blocks;
+    });
+}
+
+int azh_time_resident_tower(azh_runner* r, int slot, int B, int iters, int stem, float* ms) {
+    return guarded([&] {
+        if (!r || !ms || iters < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad timing arguments");
+        const Shape& sh = r->shape;
+        if (!azh::residentTowerSupported(sh.n, sh.F, sh.P) || (!r->tower.ok && sh.blocks > 0))
+            throw Error(AZH_ERR_ARGUMENT, "hip: the board-resident tower does not take this network");
+        r->checkBatch(B);
+        const SlotClaim held = r->claimIdle(slot);
+        Slot& s = held.slot;
+        *ms = timeOnStream(s.stream, iters,
+                           [&] { r->launchResident(r->slotBuffers(s, 0), B, s.stream, sh.blocks, stem != 0); });
+    });
+}
+
+int azh_pass_form(azh_runner* r, int B, int alone, int* form) {
+    return guarded([&] {
+        if (!r || !form) throw Error(AZH_ERR_ARGUMENT, "hip: no runner or no output");
+        r->checkBatch(B);
+        *form = (r->useSmallTower(B) ? 1 : 0) | (r->useResidentTower(B, alone != 0) ? 2 : 0) |
+                (r->splitPass(B, alone != 0) ? 4 : 0);
     });
 }
 

@@ -39,6 +39,11 @@ class Workload:
         macs = F * 9 * P * A + 2 * blocks * F * 9 * F * A + 2 * F * A + 2 * A * (A + 1) + F * A + A * V + V
         return 2 * macs
 
+    def stem_conv_flops(self, B):
+        """The stem convolution (2H + 2 input planes to F channels) over B positions."""
+        n, H, blocks, F, V = self.cfg
+        return 2.0 * F * 9 * (2 * H + 2) * n * n * B
+
     def trunk_conv_flops(self, B):
         """One residual-tower convolution over B positions."""
         n, H, blocks, F, V = self.cfg

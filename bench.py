@@ -2,14 +2,16 @@
 
 A step is one forward pass of the network over one batch of synthetic
 positions already resident in HBM (the pass replayed as its captured
-hipGraph; a batch that would leave part of a round of workgroups idle,
-the headline one included, runs as two half-batch chains on the slot's two
-streams, forked and joined inside the graph). Default workload: 19x19, 10
-residual blocks of 128 filters, batch 256 (the headline configuration).
-Prints one JSON line: throughput, the dominant kernel's roofline (the
-residual-tower 3x3 convolution: one launch over the whole batch timed live
-with HIP events on its stream, and beside it the tower's effective time per
-layer as the pass runs it), and the CPU
+hipGraph). At 19x19 and 128 filters a batch that fills its rounds of one
+workgroup per CU, the headline one included, runs the stem and the tower
+as one launch with each board resident in a workgroup; other large
+batches run as two half-batch chains on the slot's two streams, forked and
+joined inside the graph. Default workload: 19x19, 10 residual blocks of 128
+filters, batch 256 (the headline configuration). Prints one JSON line:
+throughput, the dominant kernel's roofline (the board-resident launch, or
+the residual-tower 3x3 convolution's launch over the whole batch, timed
+live with HIP events on its stream, and beside it the tower's effective
+time per layer as the pass runs it), and the CPU
 baseline (the oracle's single-threaded blas pass, one worker per host core
 at batch 8, as the reference bench's "cpu (blas)" row).
 
@@ -74,10 +76,19 @@ def parse():
     return ap.parse_args()
 
 
+# The committed rocprofv3 counter summaries, per dominant kernel.
+TRAFFIC_PROFILES = {
+    "conv3x3Tower": "conv3x3_tower_19x19_b256_hbm_traffic.txt",
+    "convTowerResident": "resident_tower_19x19_b256_hbm_traffic.txt",
+}
+
+
 def traffic_from_profile(workload_name, kernel_hash, kernel):
-    """HBM bytes per launch of the tower convolution, from the committed
+    """HBM bytes per launch of the dominant kernel, from the committed
     rocprofv3 counter summary of the same kernel and sources, or None."""
-    path = os.path.join(ROOT, "profiles", "conv3x3_tower_19x19_b256_hbm_traffic.txt")
+    if kernel not in TRAFFIC_PROFILES:
+        return None
+    path = os.path.join(ROOT, "profiles", TRAFFIC_PROFILES[kernel])
     if not os.path.exists(path):
         return None
     vals = {}
@@ -294,13 +305,24 @@ def main():
         # median of single passes, each timed on its own.
         ev_ms = r.time_passes(0, B, args.steps) / args.steps
         ev_median_ms = statistics.median(r.time_passes(0, B, 1) for _ in range(args.steps))
-        # The dominant kernel: the residual tower's 3x3 convolutions, timed as
-        # the pass runs them (every block's two launches in order).
+        # The dominant kernel. A pass alone whose batch fills its rounds of
+        # one workgroup per CU (the headline one) runs the stem and the tower
+        # as one board-resident launch: timed as the pass launches it. Else
+        # the tower's per-layer convolutions, one launch per layer over the
+        # whole batch (timed either way, for the per-layer kernel's figure).
+        # Each timing runs once untimed first: a kernel's first launch in the
+        # process also loads it.
+        resident = bool(r.pass_form(B) & r.FORM_RESIDENT)
+        r.time_tower_convs(0, B, 1)
         tower_ms, launches, layers = r.time_tower_convs(0, B, args.conv_iters)
-        conv_ms = tower_ms / launches
-        layers_per_launch = layers // launches
-        # The tower as the pass runs it (two half-batch chains on two streams
-        # where the pass splits): the effective time per layer of the batch.
+        layer_launch_ms = tower_ms / launches
+        if resident:
+            r.time_resident_tower(0, B, 1, stem=True)
+            conv_ms = r.time_resident_tower(0, B, args.conv_iters, stem=True) / args.conv_iters
+        # The tower as the pass runs it (board-resident, or two half-batch
+        # chains on two streams where the pass splits): the effective time
+        # per layer of the batch.
+        r.time_tower_layers(0, B, 1)
         pass_tower_ms, pass_layers = r.time_tower_layers(0, B, args.conv_iters)
         layer_ms = pass_tower_ms / pass_layers
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
@@ -328,10 +350,16 @@ def main():
         pos = None if args.no_positions else positions_leg(
             r, w, B, args.seen, passes=None if args.no_two_slot else max(8, args.steps))
 
-    # One launch runs layers_per_launch layers of the tower (one).
-    conv_flops = w.trunk_conv_flops(B) * layers_per_launch
+    layer_launch_flops = w.trunk_conv_flops(B) * (layers // launches)
+    if resident:
+        conv_flops = w.stem_conv_flops(B) + w.trunk_conv_flops(B) * 2 * blocks
+        kernel_name = (f"convTowerResident (the stem and the residual tower, each board resident in one workgroup: "
+                       f"one launch = the pass's {1 + 2 * blocks} convolutions over the batch)")
+    else:
+        conv_ms = layer_launch_ms
+        conv_flops = layer_launch_flops
+        kernel_name = "conv3x3Tower (residual tower, one launch = one layer over the batch)"
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
-    kernel_name = "conv3x3Tower (residual tower, one launch = one layer over the batch)"
     pass_tflops = w.flops_per_position() * B / (ms_per_step * 1e-3) / 1e12
     # "..., kernels <all> (conv <conv>)": the traffic profile is keyed by the convolution's own hash.
     kernel_hash = azgo_hip.describe().rsplit("(conv ", 1)[-1].rstrip(")")
@@ -379,6 +407,13 @@ def main():
             "per_layer_ms": round(layer_ms, 4),
             "per_layer_frac": round(w.trunk_conv_flops(B) / (layer_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
             "flops_per_launch": conv_flops,
+            # The per-layer convolution kernel over the whole batch (the
+            # dominant kernel where the pass launches per layer).
+            "layer_launch": {
+                "kernel": "conv3x3Tower",
+                "avg_launch_ms": round(layer_launch_ms, 4),
+                "frac": round(layer_launch_flops / (layer_launch_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+            },
         },
         "device": azgo_hip.describe(),
     }

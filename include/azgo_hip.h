@@ -296,6 +296,16 @@ int azh_set_graphs(azh_runner* r, int enabled);
  * hook. */
 int azh_set_small_tower(azh_runner* r, int enabled);
 
+/* Whether a 19x19 pass of a 113-128 channel network runs its stem and
+ * residual tower as one launch with each board resident in one workgroup
+ * from the first layer to the last: 0 never (one launch per layer), 1 for a
+ * pass enqueued while no other is in flight whose batch fills its rounds of
+ * one workgroup per CU to at least 97% (default), 2 at every batch. All
+ * give the same bits. Read when a pass is enqueued: set it while
+ * no other thread is beginning a pass. No counterpart in the reference (its
+ * CUDA runner launches per layer); a test hook. */
+int azh_set_resident_tower(azh_runner* r, int mode);
+
 /* ---------------------------------------------------------------- device-resident passes (measurement) */
 
 /* Copies the first B positions of the slot's pinned input to its device
@@ -312,10 +322,25 @@ int azh_fetch(azh_runner* r, int slot, int B);
  * total milliseconds. */
 int azh_time_passes(azh_runner* r, int slot, int B, int iters, float* ms);
 /* HIP events on the slot's stream around `iters` runs of the residual
- * tower as the pass runs it (every block's two convolutions, in order, on
- * the slot's staged data): total ms, the number of launches timed and the
- * number of layers they ran, for the dominant kernel's average launch time. */
+ * tower as per-layer launches over the whole batch on one stream (every
+ * block's two convolutions, in order, on the slot's staged data): total
+ * ms, the number of launches timed and the number of layers they ran, for
+ * the per-layer convolution's average launch time. */
 int azh_time_tower_convs(azh_runner* r, int slot, int B, int iters, float* ms, int* launches, int* layers);
+
+/* HIP events on the slot's stream around `iters` board-resident launches
+ * over B boards (azh_set_resident_tower), with the stem first when `stem`
+ * is nonzero (as a pass runs it) or the tower alone on the slot's staged
+ * trunk: total ms. Refused for a network the resident tower does not take
+ * (19x19, 113-128 channels, up to 32 input planes). */
+int azh_time_resident_tower(azh_runner* r, int slot, int B, int iters, int stem, float* ms);
+
+/* How a pass of B boards runs, as enqueued alone on the device (alone
+ * nonzero) or beside another pass in flight: a mask of 1 (the small-board
+ * pass in one launch), 2 (the stem and the tower board-resident in one
+ * launch) and 4 (two half-batch chains on the slot's two streams); 0: one
+ * launch per layer on one stream. */
+int azh_pass_form(azh_runner* r, int B, int alone, int* form);
 
 /* HIP events on the slot's stream around `iters` runs of the residual
  * tower as the pass runs it: one stream, or for a large batch two

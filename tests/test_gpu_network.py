@@ -276,6 +276,74 @@ def test_small_tower_equals_per_layer_launches(hip, cfg, B):
             assert bitwise_equal(a, b)
 
 
+@pytest.mark.parametrize("cfg,B", [
+    (O.make_cfg(19, 10, 128), 256),   # the headline batch: the default takes it
+    (O.make_cfg(19, 10, 128), 1),
+    (O.make_cfg(19, 2, 128), 300),    # boards past the first round of workgroups
+    (O.make_cfg(19, 2, 120, value_hidden=16, ownership=1), 5),   # a part-filled last block of channels
+    (O.make_cfg(19, 1, 128, history=3), 3),    # 8 input planes: one short stem chunk
+    (O.make_cfg(19, 1, 128, history=7), 2),    # 16: one whole chunk
+    (O.make_cfg(19, 0, 128), 4),      # no residual blocks: the stem alone
+])
+def test_resident_tower_equals_per_layer_launches(hip, cfg, B):
+    """A 19x19 pass with each board resident in one workgroup from the stem
+    to the last layer gives the bits of the per-layer launches, graph and
+    eager, with the heads (ownership included) after it."""
+    net = O.random_network(cfg, 611)
+    w = O.Workload(0, "resident", cfg, B, 0.3, 0.3)
+    inp, _ = O.workload_inputs(w, B)
+    with _runner(hip, net, B) as r:
+        r.set_resident_tower(2)
+        resident = r.infer(inp)
+        r.set_resident_tower(0)
+        per_layer = r.infer(inp)
+        r.set_graphs(False)
+        eager = r.infer(inp)
+        r.set_resident_tower(2)
+        resident_eager = r.infer(inp)
+        r.set_resident_tower(1)
+        default = r.infer(inp)
+    for got in (per_layer, eager, resident_eager, default):
+        assert len(got) == len(resident)
+        for a, b in zip(got, resident):
+            assert bitwise_equal(a, b)
+
+
+def test_resident_tower_mode_refused(hip):
+    net = O.random_network(O.make_cfg(5, 1, 16), 612)
+    with _runner(hip, net, 2) as r:
+        for bad in (-1, 3):
+            with pytest.raises(hip.HipError):
+                r.set_resident_tower(bad)
+        with pytest.raises(hip.HipError):
+            r.time_resident_tower(0, 2, 1)   # 5x5: not a network the resident tower takes
+
+
+def test_pass_forms(hip):
+    """How a pass runs, on the MI355X's 256 CUs: the board-resident tower for
+    a pass alone whose batch fills its rounds of one workgroup per CU, the
+    half-batch chains beside another pass or on a part-filled round, the
+    small-board pass in one launch on 9x9 at 64 channels past 128 boards."""
+    net = O.random_network(O.make_cfg(19, 2, 128), 613)
+    with _runner(hip, net, 512) as r:
+        assert r.pass_form(256) == r.FORM_RESIDENT
+        assert r.pass_form(512) == r.FORM_RESIDENT
+        assert r.pass_form(256, alone=False) == r.FORM_SPLIT
+        assert r.pass_form(240) == r.FORM_SPLIT
+        assert r.pass_form(1) == 0
+        r.set_resident_tower(2)
+        assert r.pass_form(1) == r.FORM_RESIDENT and r.pass_form(256, alone=False) == r.FORM_RESIDENT
+        r.set_resident_tower(0)
+        assert r.pass_form(256) == r.FORM_SPLIT
+        r.set_resident_tower(1)
+        r.input(0)[:256] = O.workload_inputs(O.Workload(0, "forms", net.cfg, 256, 0.3, 0.3), 256)[0]
+        r.stage(0, 256)
+        assert r.time_resident_tower(0, 256, 2) > 0 and r.time_resident_tower(0, 256, 2, stem=False) > 0
+    net9 = O.random_network(O.make_cfg(9, 1, 64), 614)
+    with _runner(hip, net9, 256) as r:
+        assert r.pass_form(256) == r.FORM_SMALL
+
+
 @pytest.mark.parametrize("history,B", [(8, 256), (7, 256), (9, 256), (16, 256), (8, 40), (3, 5)])
 def test_input_plane_counts_parity(hip, history, B):
     """Networks of 2H + 2 input planes around the stem's chunking (18: a
