@@ -126,6 +126,7 @@ def load():
             "azh_probe_trunk": ([vp, f32, C.c_int, C.c_int, f32], C.c_int),
             "azh_probe_fill": ([f32, C.c_size_t, C.c_float, C.c_size_t], C.c_int),
             "azh_probe_copy": ([C.c_size_t, C.c_int, f32], C.c_int),
+            "azh_probe_mfma": ([C.c_int, C.c_int, f32, P(C.c_double)], C.c_int),
             "azh_set_hub_chaos_seed": ([C.c_uint64], None),
             "azh_hub_chaos_seed": ([], C.c_uint64),
             "azh_fail_passes_after": ([C.c_int], None),
@@ -557,6 +558,14 @@ def probe_fill(data, n, value, tail=0):
     data = _f32(data).copy()
     _check(load().azh_probe_fill(_f(data), n, value, tail))
     return data
+
+
+def probe_mfma(chain, iters):
+    """(total ms, flops per launch) of `iters` launches of dependent MFMA
+    chains, one 8-wave workgroup per CU."""
+    ms, flops = C.c_float(), C.c_double()
+    _check(load().azh_probe_mfma(chain, iters, C.byref(ms), C.byref(flops)))
+    return ms.value, flops.value
 
 
 def probe_copy(nbytes, iters):

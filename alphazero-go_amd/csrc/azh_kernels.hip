@@ -214,6 +214,24 @@ __global__ void fillKernel(float* data, size_t n, float value) {
     if (i < n) data[i] = value;
 }
 
+// The matrix units' rate with nothing else in the way: 8 waves per
+// workgroup (two per SIMD), each a dependent chain of 4 * chain
+// v_mfma_f32_16x16x4_f32 on one accumulator (a dependent chain issues one
+// MFMA per 32 cycles, as independent ones do). The operands are tiny, so
+// the sums stay finite; one float per thread is written so the chain is
+// kept.
+__global__ __launch_bounds__(512) void mfmaChainKernel(float* out, int chain) {
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float a = 1.0f + threadIdx.x * 1e-7f, b = 1e-9f;
+    for (int i = 0; i < chain; ++i) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+    }
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
+}
+
 } // namespace
 
 // ------------------------------------------------------------------ host side
@@ -437,6 +455,12 @@ hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream) {
     if (khz <= 0) khz = 100000;
     const unsigned long long ticks = nanoseconds * (unsigned long long)khz / 1000000ull;
     hipLaunchKernelGGL(spinKernel, dim3(1), dim3(1), 0, stream, ticks);
+    return hipGetLastError();
+}
+
+hipError_t launchMfmaChains(float* out, int workgroups, int chain, hipStream_t stream) {
+    if (workgroups < 1 || chain < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mfmaChainKernel, dim3(workgroups), dim3(kMfmaChainThreads), 0, stream, out, chain);
     return hipGetLastError();
 }
 

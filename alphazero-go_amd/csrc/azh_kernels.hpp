@@ -117,4 +117,10 @@ hipError_t launchPriors(const float* logits, const uint8_t* legal, const uint8_t
 hipError_t launchSpin(unsigned long long nanoseconds, hipStream_t stream);
 hipError_t launchFill(float* data, size_t n, float value, hipStream_t stream);
 
+// The fp32 matrix units' rate with nothing else in the way: `workgroups`
+// workgroups of kMfmaChainThreads threads, each wave a dependent chain of
+// 4 * chain 16x16x4 MFMAs (2048 flops each); out holds one float per thread.
+constexpr int kMfmaChainThreads = 512;
+hipError_t launchMfmaChains(float* out, int workgroups, int chain, hipStream_t stream);
+
 } // namespace azh

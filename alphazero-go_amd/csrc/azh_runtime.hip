@@ -2246,6 +2246,33 @@ int azh_probe_fill(float* data, size_t n, float value, size_t tail) {
     });
 }
 
+int azh_probe_mfma(int chain, int iters, float* ms, double* flops) {
+    return guarded([&] {
+        if (!ms || !flops || iters < 1 || chain < 1) throw Error(AZH_ERR_ARGUMENT, "hip: bad MFMA probe arguments");
+        requireContext();
+        const int workgroups = azh::deviceCUs();
+        float* out = nullptr;
+        check(hipMalloc(&out, (size_t)workgroups * azh::kMfmaChainThreads * sizeof(float)), "hipMalloc");
+        hipStream_t st = nullptr;
+        hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+        float t = 0.0f;
+        if (e == hipSuccess) {
+            try {
+                check(azh::launchMfmaChains(out, workgroups, chain, st), "MFMA chains");   // untimed: loads the kernel
+                t = timeOnStream(st, iters, [&] { check(azh::launchMfmaChains(out, workgroups, chain, st), "MFMA chains"); });
+            } catch (const Error& err) {
+                e = hipErrorUnknown;
+                gLastError = err.what();
+            }
+        }
+        if (st) (void)hipStreamDestroy(st);
+        (void)hipFree(out);
+        check(e, "MFMA probe");
+        *ms = t;
+        *flops = (double)workgroups * (azh::kMfmaChainThreads / 64) * 4.0 * chain * 2048.0;
+    });
+}
+
 int azh_probe_copy(size_t bytes, int iters, float* ms) {
     return guarded([&] {
         if (!ms || iters < 1 || bytes == 0) throw Error(AZH_ERR_ARGUMENT, "hip: bad copy probe arguments");

@@ -17,11 +17,14 @@ at batch 8, as the reference bench's "cpu (blas)" row).
 
   python bench.py [--steps K] [--warmup W] [--workload 3] [--no-cpu] [--no-positions]
 
-Two more modes serve the committed profiles (each prints one line):
+Three more modes serve the committed profiles (each prints one line):
 
   python bench.py --mode copy-calibration [--mib 256] [--conv-iters 5]
       a plain device-to-device copy of known size, for scaling rocprofv3's
       FETCH_SIZE / WRITE_SIZE readings to bytes;
+  python bench.py --mode mfma-calibration [--conv-iters 5]
+      dependent MFMA chains on every SIMD with nothing else in the way: the
+      fp32 matrix rate the chip holds, beside the published peak;
   python bench.py --mode stem-heads [--workload 3] [--batch B] [--conv-iters 10]
       whole-batch launches of the stem convolution and the heads on one
       stream (in a pass of a large batch they run as two concurrent
@@ -71,7 +74,7 @@ def parse():
     ap.add_argument("--no-two-slot", action="store_true",
                     help="skip the runner-kept-full rate (its two slots overlap kernels; for kernel-trace profiles)")
     ap.add_argument("--seen", type=int, default=200, help="superko hashes per position")
-    ap.add_argument("--mode", default="pass", choices=["pass", "copy-calibration", "stem-heads"])
+    ap.add_argument("--mode", default="pass", choices=["pass", "copy-calibration", "mfma-calibration", "stem-heads"])
     ap.add_argument("--mib", type=int, default=256, help="copy-calibration: MiB copied per launch")
     return ap.parse_args()
 
@@ -165,6 +168,20 @@ def copy_calibration(mib, iters):
     print(json.dumps({"mode": "copy-calibration", "bytes_per_copy": nbytes, "copies": iters,
                       "ms_per_copy": round(ms / iters, 4),
                       "gb_s_read_plus_write": round(2 * nbytes / (ms / iters * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def mfma_calibration(iters):
+    """The fp32 matrix units' rate with nothing else in the way: one 8-wave
+    workgroup per CU, each wave a dependent chain of 80,000 16x16x4 MFMAs
+    (one per 32 cycles per SIMD): the clock the chip holds under a full
+    MFMA load, against the 2.4 GHz of the published peak."""
+    import azgo_hip
+    ms, flops = azgo_hip.probe_mfma(20000, iters)
+    tf = flops / (ms / iters * 1e-3) / 1e12
+    print(json.dumps({"mode": "mfma-calibration", "launches": iters, "ms_per_launch": round(ms / iters, 4),
+                      "flops_per_launch": flops, "tflops": round(tf, 2),
+                      "frac_of_published_peak": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                      "implied_clock_ghz": round(2.4 * tf / PEAK_FP32_MFMA_TFLOPS, 3)}), flush=True)
 
 
 def stem_heads(workload, B, iters):
@@ -274,6 +291,8 @@ def main():
         raise SystemExit(f"bench.py: no usable gfx950 GPU: {why}")
     if args.mode == "copy-calibration":
         return copy_calibration(args.mib, args.conv_iters)
+    if args.mode == "mfma-calibration":
+        return mfma_calibration(args.conv_iters)
     if args.mode == "stem-heads":
         return stem_heads(args.workload, args.batch, args.conv_iters)
     w = W.WORKLOADS[args.workload]
@@ -325,6 +344,10 @@ def main():
         r.time_tower_layers(0, B, 1)
         pass_tower_ms, pass_layers = r.time_tower_layers(0, B, args.conv_iters)
         layer_ms = pass_tower_ms / pass_layers
+        # The matrix units' measured ceiling: dependent MFMA chains, one
+        # 8-wave workgroup per CU, nothing else in the way.
+        ceil_ms, ceil_flops = azgo_hip.probe_mfma(20000, 3)
+        mfma_ceiling = ceil_flops / (ceil_ms / 3 * 1e-3) / 1e12
         # PCIe-inclusive round trips (pinned H2D, pass, D2H, wait), for the record.
         rt_ms = r.time_round_trips(0, B, max(3, args.steps // 5)) / max(3, args.steps // 5)
         rt_median_ms = statistics.median(r.time_round_trips(0, B, 1) for _ in range(max(3, args.steps // 5)))
@@ -407,6 +430,11 @@ def main():
             "per_layer_ms": round(layer_ms, 4),
             "per_layer_frac": round(w.trunk_conv_flops(B) / (layer_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
             "flops_per_launch": conv_flops,
+            # The published peak assumes 2.4 GHz; under a full MFMA load the
+            # chip runs slower. Beside `frac`: the same kernel against the
+            # rate measured for MFMAs alone in this run.
+            "measured_mfma_ceiling": round(mfma_ceiling, 2),
+            "frac_of_measured_ceiling": round(achieved / mfma_ceiling, 4),
             # The per-layer convolution kernel over the whole batch (the
             # dominant kernel where the pass launches per layer).
             "layer_launch": {

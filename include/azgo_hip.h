@@ -405,6 +405,12 @@ int azh_probe_fill(float* data, size_t n, float value, size_t tail);
  * counters), repeated `iters` times; total ms. */
 int azh_probe_copy(size_t bytes, int iters, float* ms);
 
+/* The fp32 matrix units' rate with nothing else in the way (the measured
+ * ceiling beside the published peak): one workgroup of 8 waves per CU, each
+ * wave a dependent chain of 4 * chain v_mfma_f32_16x16x4_f32, launched
+ * `iters` times; total ms and the flops of one launch. */
+int azh_probe_mfma(int chain, int iters, float* ms, double* flops);
+
 /* ---------------------------------------------------------------- test hooks (cuda_probe, include/azgo/cuda.hpp:138-155) */
 
 /* Hub chaos seed WorkerEvaluators reads (cuda_probe::setHubChaosSeed). */

@@ -787,6 +787,18 @@ def test_fill_probe_tail_untouched(hip):
     assert np.all(out[:16] == 2.5) and np.array_equal(out[16:], data[16:])
 
 
+def test_mfma_probe(hip):
+    """The matrix-rate probe: one 8-wave workgroup per CU (256 on the
+    MI355X), each wave 4 x chain MFMAs of 2048 flops, at a rate no higher
+    than the published 157.3 TFLOP/s peak and not far below it."""
+    ms, flops = hip.probe_mfma(2000, 2)
+    assert flops == 256 * 8 * 4 * 2000 * 2048
+    tf = flops / (ms / 2 * 1e-3) / 1e12
+    assert 100.0 < tf <= 157.3 * 1.01, tf
+    with pytest.raises(hip.HipError):
+        hip.probe_mfma(0, 1)
+
+
 def test_describe(hip):
     d = hip.describe()
     assert "gfx950" in d and "kernels" in d
