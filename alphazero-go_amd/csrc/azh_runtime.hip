@@ -1209,7 +1209,20 @@ struct azh_runner {
     // alone: no other pass in flight (othersIdle).
     void launchPass(Slot& s, int B, hipStream_t stream, int blocksToRun, bool heads, bool alone) {
         if (useResidentTower(B, alone)) {
-            const PassBuffers io = slotBuffers(s, 0);
+            launchPassOn(slotBuffers(s, 0), B, stream, blocksToRun, heads, alone);
+            return;
+        }
+        const bool small = useSmallTower(B);
+        overHalves(s, B, stream, alone, [&](int b0, int Bp, hipStream_t st) {
+            launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp, alone), st, blocksToRun, heads, small);
+        });
+    }
+
+    // A pass over io's B boards on one stream (no half-batch chains), in
+    // the form the runner takes for it otherwise: board-resident, the
+    // small-board pass, or per-layer launches.
+    void launchPassOn(const PassBuffers& io, int B, hipStream_t stream, int blocksToRun, bool heads, bool alone) {
+        if (useResidentTower(B, alone)) {
             launchResident(io, B, stream, blocksToRun, true);
             if (heads)
                 check(azh::launchHeads(io.x, weights.heads, io.act, io.logits, io.values, io.own, B, shape.n, shape.F,
@@ -1217,10 +1230,8 @@ struct azh_runner {
                       "heads");
             return;
         }
-        const bool small = useSmallTower(B);
-        overHalves(s, B, stream, alone, [&](int b0, int Bp, hipStream_t st) {
-            launchPassPart(slotBuffers(s, b0), Bp, B, partTiling(B, Bp, alone), st, blocksToRun, heads, small);
-        });
+        launchPassPart(io, B, B, azh::chooseConvTiling(shape.F, B, shape.n, alone), stream, blocksToRun, heads,
+                       useSmallTower(B));
     }
 
     // The tower as the pass runs it, on slot s's staged trunk (the effective
@@ -1765,9 +1776,8 @@ int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, f
         float* mid = x + alignFloats(azh::quadFloats(B, sh.F, sh.A));
         float* act = mid + alignFloats(azh::quadFloats(B, sh.F, sh.A));
         // Alone when none of the runner's slots has a pass in flight.
-        r->launchPassPart(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B, B,
-                          azh::chooseConvTiling(sh.F, B, sh.n, r->othersIdle(nullptr)),
-                          static_cast<hipStream_t>(stream), sh.blocks, true, r->useSmallTower(B));
+        r->launchPassOn(azh_runner::PassBuffers{input, x, mid, act, logits, values, ownership}, B,
+                        static_cast<hipStream_t>(stream), sh.blocks, true, r->othersIdle(nullptr));
     });
 }
 

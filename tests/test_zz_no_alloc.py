@@ -88,10 +88,13 @@ def _noalloc(hip_rt, r, cfg, inp, stream, ownership=False):
 
 
 # (network, first batch, second batch, ownership): the 19x19 10x128
-# benchmark network through the per-layer launches, the 5x5 one through the
-# one-launch small-board pass, a 9x9 network with the ownership head.
+# benchmark network through the per-layer launches, a 19x19 128-channel
+# network through the board-resident tower at 256 boards (then per layer at
+# 13), the 5x5 one through the one-launch small-board pass, a 9x9 network
+# with the ownership head.
 CASES = [
     ("19x19 10x128", lambda: O.init_network(O.WORKLOADS[3].cfg), O.WORKLOADS[3], 48, 13, False),
+    ("19x19 2x128 resident", lambda: O.random_network(O.make_cfg(19, 2, 128), 72), O.WORKLOADS[3], 256, 13, False),
     ("5x5 4x32", lambda: O.init_network(O.WORKLOADS[1].cfg), O.WORKLOADS[1], 8, 3, False),
     ("9x9 2x16 own", lambda: O.random_network(O.make_cfg(9, 2, 16, value_hidden=16, ownership=1), 71),
      O.WORKLOADS[2], 6, 2, True),
