@@ -405,8 +405,9 @@ class Runner:
         _check(self.lib.azh_set_small_tower(self.h, int(enabled)))
 
     def set_resident_tower(self, mode):
-        """0: per-layer launches; 1: the board-resident tower where the batch
-        fills its rounds of CUs (default); 2: wherever the network allows it."""
+        """0: per-layer launches; 1: the board-resident tower for a pass alone
+        whose batch fills its rounds of CUs (default); 2: wherever the network
+        allows it."""
         _check(self.lib.azh_set_resident_tower(self.h, int(mode)))
 
     # ---- slot staging (the hub's view)

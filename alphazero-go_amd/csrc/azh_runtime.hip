@@ -1093,14 +1093,17 @@ struct azh_runner {
     // Whether a pass of B runs its stem and tower as one board-resident
     // launch (alone: no other pass in flight, othersIdle). A board's tower
     // takes the same time on its CU whatever the batch (19x19 10x128: 3.90
-    // ms per pass up to 256 boards), so a round of workgroups part-filled
-    // idles CUs for all of it, while the per-layer launches shrink with the
-    // batch: taken when the rounds are at least 97% full (per pass at 256
-    // boards 3.90 against 3.97 ms, at 512 7.76 against 7.79; at 240 3.90
-    // against 3.87). Not with another pass in flight: its workgroups hold
-    // every CU's registers for a whole tower, so the other pass's kernels
-    // (heads included) wait for them (two slots kept full: 63.7k against
-    // 64.7k positions/s).
+    // ms per pass up to 256 boards, 7.77 up to 512), so a part-filled round
+    // of workgroups idles CUs for all of it, while the per-layer launches
+    // shrink with the batch. Per pass against the per-layer launches (256
+    // CUs): 256 boards 3.905 against 3.970 ms, 250 3.901 / 3.940, 244
+    // 3.886 / 3.912, 240 3.883 / 3.858; 512 7.774 / 7.816, 504 7.770 /
+    // 7.710; 768 11.651 / 11.751, 746 11.657 / 11.695, 740 11.661 / 11.612.
+    // So taken for one round from 95% of the CUs, and for more rounds only
+    // when they are full. Not with another pass in flight: its workgroups
+    // hold every CU's registers for a whole tower, so the other pass's
+    // kernels (heads included) wait for them (two slots kept full: 63.7k
+    // against 64.7k positions/s).
     bool useResidentTower(int B, bool alone) const {
         const Shape& sh = shape;
         if (residentTower == 0 || (!tower.ok && sh.blocks > 0) || B < 1 ||
@@ -1109,7 +1112,7 @@ struct azh_runner {
         if (residentTower == 2) return true;
         const long cus = azh::deviceCUs();
         const long rounds = (B + cus - 1) / cus;
-        return alone && 100L * B >= 97L * rounds * cus;
+        return alone && (rounds == 1 ? 20L * B >= 19L * cus : B == rounds * cus);
     }
 
     // The stem (when asked) and the tower's first `blocksToRun` blocks over

@@ -299,9 +299,9 @@ int azh_set_small_tower(azh_runner* r, int enabled);
 /* Whether a 19x19 pass of a 113-128 channel network runs its stem and
  * residual tower as one launch with each board resident in one workgroup
  * from the first layer to the last: 0 never (one launch per layer), 1 for a
- * pass enqueued while no other is in flight whose batch fills its rounds of
- * one workgroup per CU to at least 97% (default), 2 at every batch. All
- * give the same bits. Read when a pass is enqueued: set it while
+ * pass enqueued while no other is in flight whose batch gives one
+ * workgroup to at least 95% of the CUs, or to every CU in each of two or
+ * more rounds (default), 2 at every batch. All give the same bits. Read when a pass is enqueued: set it while
  * no other thread is beginning a pass. No counterpart in the reference (its
  * CUDA runner launches per layer); a test hook. */
 int azh_set_resident_tower(azh_runner* r, int mode);

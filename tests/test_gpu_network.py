@@ -321,15 +321,18 @@ def test_resident_tower_mode_refused(hip):
 
 def test_pass_forms(hip):
     """How a pass runs, on the MI355X's 256 CUs: the board-resident tower for
-    a pass alone whose batch fills its rounds of one workgroup per CU, the
+    a pass alone whose batch gives one workgroup to 95% of the CUs (or to
+    every CU in each of several rounds), the
     half-batch chains beside another pass or on a part-filled round, the
     small-board pass in one launch on 9x9 at 64 channels past 128 boards."""
     net = O.random_network(O.make_cfg(19, 2, 128), 613)
     with _runner(hip, net, 512) as r:
         assert r.pass_form(256) == r.FORM_RESIDENT
+        assert r.pass_form(244) == r.FORM_RESIDENT   # one round: from 95% of the CUs
         assert r.pass_form(512) == r.FORM_RESIDENT
         assert r.pass_form(256, alone=False) == r.FORM_SPLIT
         assert r.pass_form(240) == r.FORM_SPLIT
+        assert r.pass_form(504) == r.FORM_SPLIT      # two rounds: only when full
         assert r.pass_form(1) == 0
         r.set_resident_tower(2)
         assert r.pass_form(1) == r.FORM_RESIDENT and r.pass_form(256, alone=False) == r.FORM_RESIDENT
