@@ -2271,8 +2271,9 @@ int azh_probe_mfma(int chain, int iters, float* ms, double* flops) {
         float t = 0.0f;
         if (e == hipSuccess) {
             try {
-                check(azh::launchMfmaChains(out, workgroups, chain, st), "MFMA chains");   // untimed: loads the kernel
-                t = timeOnStream(st, iters, [&] { check(azh::launchMfmaChains(out, workgroups, chain, st), "MFMA chains"); });
+                auto launch = [&] { check(azh::launchMfmaChains(out, workgroups, chain, st), "MFMA chains"); };
+                launch();   // untimed: loads the kernel
+                t = timeOnStream(st, iters, launch);
             } catch (const Error& err) {
                 e = hipErrorUnknown;
                 gLastError = err.what();
