@@ -6,7 +6,7 @@
 // engine tests (tests/test_cuda.cpp:1022-1348, tests/test_inference_hub.cpp:272-628).
 //
 //   hub_hip_driver <scenario>   scenario: chaos | failure | memory | refusals | drain | ownership | throughput
-//                                         | names | selfplay | arena
+//                                         | names | engines | selfplay | arena
 //
 // Prints "PASS <scenario>" and exits 0, or prints what failed and exits 1.
 #include <algorithm>
@@ -25,6 +25,7 @@
 #include "azgo/arena.hpp"
 #include "azgo/backend.hpp"
 #include "azgo/config.hpp"
+#include "azgo/engines.hpp"
 #include "azgo/inference_hub.hpp"
 #include "azgo/network.hpp"
 #include "azgo/replay_buffer.hpp"
@@ -473,6 +474,114 @@ void names() {
     expect(evaluators.evaluations() == workers * per, "the hub counted every position");
 }
 
+// The engine-spec sites (oracle/hip_names.patch: src/engines.cpp, the hosts
+// file's hip_workers, src/coordinator.cpp's memory check) as a run's
+// configuration meets them. A config naming hip engines parses and prints
+// back unchanged, as the reference checks for cuda (test_config_arena_engines,
+// tests/test_config.cpp:764-780); hip_workers sets a hip engine's workers as
+// cuda_workers sets a cuda engine's, and without it every game of the slice
+// runs at once (tests/test_distributed.cpp:347-349, 411-421; dynamic shares,
+// tests/test_game_queue.cpp:241-245); the engine fingerprint names the GPU and
+// the kernels; and the groups the coordinator's preflight checks for hip
+// engines (self-play hubs of two slots beside an arena wave's one-slot hubs)
+// are refused with "lower inference_batch" when the GPU is too small. (The
+// preflight itself is not linked here: it also names build_info's functions,
+// whose source needs a CMake-generated include.)
+void engines() {
+    auto configError = [](const std::string& text) {
+        try {
+            parseConfigText(text, "e.cfg");
+        } catch (const ConfigError& e) {
+            return std::string(e.what());
+        }
+        return std::string();
+    };
+    auto hostsError = [](const std::string& text) {
+        try {
+            parseHostsText(text, "h");
+        } catch (const ConfigError& e) {
+            return std::string(e.what());
+        }
+        return std::string();
+    };
+    auto has = [](const std::string& s, const std::string& part) { return s.find(part) != std::string::npos; };
+
+    const Config c = parseConfigText("selfplay_engines = local/hip:40, pc/hip:60\narena_engines = pc/hip:300\n", "e.cfg");
+    expect(c.selfplayEngines.size() == 2 && c.selfplayEngines[0].machine == "local" &&
+               c.selfplayEngines[0].backend == "hip" && c.selfplayEngines[0].weight == 40 &&
+               c.selfplayEngines[1].machine == "pc" && c.selfplayEngines[1].backend == "hip" &&
+               c.selfplayEngines[1].weight == 60,
+           "selfplay_engines = local/hip:40, pc/hip:60 parses");
+    expect(c.arenaEngines.size() == 1 && c.arenaEngines[0].name() == "pc/hip" && c.arenaEngines[0].weight == 300 &&
+               c.arenaEngines[0].games == -1,
+           "arena_engines = pc/hip:300 parses");
+    const std::string text = configToString(c);
+    expect(has(text, "\nselfplay_engines = local/hip:40, pc/hip:60\n") && has(text, "\narena_engines = pc/hip:300\n"),
+           "the engine lists print back as written");
+    expect(configToString(parseConfigText(text, "rt")) == text, "the printed config parses to itself");
+    checkConsistency(c);
+    const Config fixed = parseConfigText("games_per_generation = 6\nselfplay_engines = pc/hip=6\n", "e.cfg");
+    expect(fixed.selfplayEngines.size() == 1 && fixed.selfplayEngines[0].games == 6, "pc/hip=6 gives a fixed count");
+    const std::string unknown = configError("selfplay_engines = pc/rocm:1\n");
+    expect(has(unknown, "e.cfg:1: selfplay_engines: ") && has(unknown, "(expected naive|blas|metal|cuda|hip)"),
+           "an unknown engine backend names hip among the choices: " + unknown);
+    const std::string runBackend = configError("backend = hip\n");
+    expect(has(runBackend, "hip is an engine only") && has(runBackend, "pc/hip:60"),
+           "a run's backend = hip points at a hip engine list: " + runBackend);
+
+    const MachineSettings pc =
+        parseHostsText("pc exe=/a workdir=/w hip_workers=48 cuda_workers=7 metal_workers=5 cpu_workers=3\n", "h")
+            .settings("pc");
+    expect(pc.hipWorkers == 48 && pc.cudaWorkers == 7, "hip_workers is read beside cuda_workers");
+    expect(engineWorkers(pc, "hip", 100, 16) == 48 && engineWorkers(pc, "hip", 20, 16) == 20,
+           "a hip engine runs hip_workers workers, at most the slice's games");
+    expect(engineWorkers(pc, "cuda", 100, 16) == 7 && engineWorkers(pc, "blas", 100, 16) == 3,
+           "hip_workers applies to hip engines only");
+    const MachineSettings plain = parseHostsText("pc exe=/a workdir=/w\n", "h").settings("pc");
+    expect(plain.hipWorkers == 0 && engineWorkers(plain, "hip", 300, 16) == kMaxArenaWorkers &&
+               engineWorkers(plain, "hip", 52, 16) == 52,
+           "without hip_workers every game of the slice at once, at most 256");
+    expect(sliceWorkers("hip", 0, 296, 16) == 256 && sliceWorkers("hip", 0, 52, 16) == 52 &&
+               sliceWorkers("hip", 9, 52, 16) == 9,
+           "a remote's hip slice: --workers, else every game at once");
+    expect(dynamicWorkers(plain, "hip", 256, 400, 18) == 64 && dynamicWorkers(plain, "hip", 1023, 2000, 18) == 256 &&
+               dynamicWorkers(pc, "hip", 256, 400, 18) == 48,
+           "dynamic shares: a quarter of the share on a hip engine, or hip_workers");
+    expect(has(hostsError("pc exe=/a workdir=/w hip_workers=-1\n"), "hip_workers") &&
+               has(hostsError("pc exe=/a workdir=/w hip_workers=257\n"), "hip_workers") &&
+               has(hostsError("pc exe=/a workdir=/w hip_workers=2 hip_workers=3\n"), "repeated"),
+           "bad hip_workers values are refused by name");
+    expect(parseHostsText("pc exe=/a workdir=/w hip_workers=0\n", "h").settings("pc").hipWorkers == 0,
+           "hip_workers = 0 is the default");
+
+    const std::string fingerprint = engineFingerprint("hip");
+    const std::string suffix = "; " + hipDescription();
+    expect(fingerprint.rfind("hip; ", 0) == 0 && fingerprint.size() > suffix.size() &&
+               fingerprint.compare(fingerprint.size() - suffix.size(), suffix.size(), suffix) == 0,
+           "the hip engine's fingerprint ends with the GPU and kernel description: " + fingerprint);
+
+    // What the coordinator's preflight checks for a pipelined run with two
+    // local hip self-play engines and a local hip arena engine over a wave of
+    // three networks: the self-play hubs beside the arena's.
+    const NetConfig net = config(19, 10, 128, 64);
+    const std::vector<GpuHubs> groups = {{2, kInferenceSlots, 256}, {3, 1, 256}};
+    hip_probe::setMemoryLimit(size_t(64) << 20);
+    std::string refused;
+    try {
+        checkHipInferenceMemory(net, groups);
+    } catch (const std::runtime_error& e) {
+        refused = e.what();
+    }
+    hip_probe::setMemoryLimit(0);
+    const std::string tail = "lower inference_batch";
+    expect(refused.size() > tail.size() && refused.compare(refused.size() - tail.size(), tail.size(), tail) == 0 &&
+               has(refused, "(5 hubs)"),
+           "self-play and arena hubs that do not fit together are refused: " + refused);
+    checkHipInferenceMemory(net, groups);   // they fit the whole GPU
+    std::printf("engines: %s | %s\n", text.substr(text.find("selfplay_engines")).substr(0, 44).c_str(),
+                fingerprint.c_str());
+}
+
 // A slice's games as the bytes its result file carries: each GameRecord
 // serialized by writeGameRecord (include/azgo/replay_buffer.hpp:47).
 std::string gameBytes(const std::vector<GameRecord>& games) {
@@ -482,52 +591,97 @@ std::string gameBytes(const std::vector<GameRecord>& games) {
     return out.str();
 }
 
-// The determinism contract of a GPU engine's self-play slice, through the
-// reference's unchanged playSelfPlayGames, MCTS and hub: the same games,
-// byte for byte, for 1, 3 and 8 workers, passes capped at 8 or 256
-// positions, and the hub's chaos mode off and on
-// (test_selfplay_slice_independent_of_workers_and_batching,
-// tests/test_cuda.cpp:1270-1298).
+// An arena wave's games as one string: each game's score and moves.
+std::string arenaMoves(const std::vector<ArenaGameResult>& games) {
+    std::string out;
+    for (const ArenaGameResult& g : games) {
+        out += std::to_string(g.scoreA) + ":";
+        for (int m : g.moves) out += std::to_string(m) + ",";
+        out += ";";
+    }
+    return out;
+}
+
+// How a GPU engine may run a slice without changing its games: the hub's
+// worker threads, the cap on a pass's positions and the hub's chaos seed
+// (random caps, shuffled requests, submission pauses).
+struct EngineSettings {
+    int workers;
+    int cap;
+    uint64_t chaos;
+};
+
+std::vector<EngineSettings> settingsGrid(const std::vector<int>& workers, const std::vector<int>& caps,
+                                         const std::vector<uint64_t>& chaos) {
+    std::vector<EngineSettings> grid;
+    for (int w : workers)
+        for (int c : caps)
+            for (uint64_t s : chaos) grid.push_back({w, c, s});
+    return grid;
+}
+
+// Plays `play(run, stats)` on the hip engine under every setting of `grid`
+// and checks that each result equals the first. Returns the first result;
+// *evaluations adds up the positions the GPU evaluated.
+template <class Play>
+std::string sameUnderEverySetting(const std::string& what, const std::vector<EngineSettings>& grid, Play play,
+                                  long long* evaluations) {
+    std::string first;
+    for (const EngineSettings& s : grid) {
+        EngineRun run;
+        run.backend = "hip";
+        run.workers = s.workers;
+        run.inferenceBatch = s.cap;
+        SliceStats stats;
+        hip_probe::setHubChaosSeed(s.chaos);
+        const std::string result = play(run, stats);
+        hip_probe::setHubChaosSeed(0);
+        const std::string label = what + " (workers " + std::to_string(s.workers) + ", cap " +
+                                  std::to_string(s.cap) + ", chaos " + std::to_string(s.chaos) + ")";
+        expect(stats.evaluations > 0, label + ": positions were evaluated on the GPU");
+        *evaluations += stats.evaluations;
+        if (&s == &grid.front()) first = result;
+        expect(result == first, label + ": the same games as the first setting");
+    }
+    return first;
+}
+
+// The determinism contract of a GPU engine's self-play slice through the
+// reference's unchanged playSelfPlayGames, MCTS and hub: the same game bytes
+// whatever the workers, pass cap and chaos. The parameters (networks, search
+// settings, seeds, the settings grid) are those of the reference's
+// test_selfplay_slice_independent_of_workers_and_batching
+// (tests/test_cuda.cpp:1270-1298).
 void selfplay() {
+    const std::vector<EngineSettings> grid = settingsGrid({1, 3, 8}, {8, 256}, {0, 21});
     for (const NetConfig& cfg : {config(5, 1, 8, 16), config(9, 2, 16, 16)}) {
         const Network net = randomNetwork(cfg, 801);
         SelfPlayConfig sp;
         sp.mcts.simulations = 32;
         sp.mcts.batchSize = 8;
         sp.temperatureMoves = 6;
-        std::string first;
-        int runs = 0;
         long long evaluations = 0;
-        for (int workers : {1, 3, 8})
-            for (int cap : {8, 256})
-                for (uint64_t chaos : {0ull, 21ull}) {
-                    hip_probe::setHubChaosSeed(chaos);
-                    EngineRun run;
-                    run.backend = "hip";
-                    run.workers = workers;
-                    run.inferenceBatch = cap;
-                    SliceStats stats;
-                    const std::string bytes = gameBytes(playSelfPlayGames(net, sp, 802, 3, 10, 6, run, &stats));
-                    hip_probe::setHubChaosSeed(0);
-                    expect(stats.evaluations > 0, "the slice evaluated positions on the GPU");
-                    evaluations += stats.evaluations;
-                    if (first.empty()) first = bytes;
-                    expect(bytes == first, "workers " + std::to_string(workers) + ", cap " + std::to_string(cap) +
-                                               ", chaos " + std::to_string(chaos) + ": the same game bytes");
-                    ++runs;
-                }
-        std::printf("selfplay %dx%d %dx%d: %d runs of 6 games, %zu bytes each, %lld positions evaluated\n",
-                    cfg.boardSize, cfg.boardSize, cfg.blocks, cfg.filters, runs, first.size(), evaluations);
+        const std::string bytes = sameUnderEverySetting(
+            "selfplay " + std::to_string(cfg.boardSize) + "x" + std::to_string(cfg.boardSize), grid,
+            [&](const EngineRun& run, SliceStats& stats) {
+                return gameBytes(playSelfPlayGames(net, sp, /*seed*/ 802, /*generation*/ 3, /*first*/ 10,
+                                                   /*count*/ 6, run, &stats));
+            },
+            &evaluations);
+        std::printf("selfplay %dx%d %dx%d: %zu settings of 6 games, %zu bytes each, %lld positions evaluated\n",
+                    cfg.boardSize, cfg.boardSize, cfg.blocks, cfg.filters, grid.size(), bytes.size(), evaluations);
         std::fflush(stdout);
     }
 }
 
 // An arena wave on the hip engine (one hub per network, several networks
-// sharing the GPU, every game at once), through the reference's unchanged
-// playArenaGames: the same games, move for move, for any workers, pass cap
-// and chaos, and slices of the wave joined play what the whole wave plays
-// (test_arena_wave_independent_of_workers_and_batching,
-// tests/test_cuda.cpp:1300-1348).
+// sharing the GPU; workers 0 = every game at once) through the reference's
+// unchanged playArenaGames: the same moves whatever the workers, pass cap and
+// chaos, and two slices of the wave played apart equal to the whole. The
+// parameters (networks, wave, search settings, the settings grid, the slice
+// boundary) are those of the reference's
+// test_arena_wave_independent_of_workers_and_batching
+// (tests/test_cuda.cpp:1300-1348).
 void arena() {
     const NetConfig cfg = config(5, 1, 8, 16);
     const Network a = randomNetwork(cfg, 811), b = randomNetwork(cfg, 812), c = randomNetwork(cfg, 813);
@@ -540,48 +694,30 @@ void arena() {
         {ArenaPlayer::network(a), ArenaPlayer::bot(8), 4, 902},
         {ArenaPlayer::network(a), ArenaPlayer::network(c), 4, 903},
     };
-    auto played = [](const std::vector<ArenaGameResult>& games) {
-        std::string out;
-        for (const ArenaGameResult& g : games) {
-            out += std::to_string(g.scoreA) + ":";
-            for (int m : g.moves) out += std::to_string(m) + ",";
-            out += ";";
-        }
-        return out;
-    };
-    std::string whole;
-    int runs = 0;
-    for (int workers : {1, 3, 0})
-        for (int cap : {8, 256})
-            for (uint64_t chaos : {0ull, 23ull}) {
-                hip_probe::setHubChaosSeed(chaos);
-                EngineRun run;
-                run.backend = "hip";
-                run.workers = workers;
-                run.inferenceBatch = cap;
-                SliceStats stats;
-                const std::string games = played(playArenaGames(waveSlice(wave, 0, 14), ac, run, &stats));
-                hip_probe::setHubChaosSeed(0);
-                expect(stats.evaluations > 0, "the wave evaluated positions on the GPU");
-                if (whole.empty()) whole = games;
-                expect(games == whole, "workers " + std::to_string(workers) + ", cap " + std::to_string(cap) +
-                                           ", chaos " + std::to_string(chaos) + ": the same games");
-                ++runs;
-            }
+    const int games = 14, cut = 5;
+    const std::vector<EngineSettings> grid = settingsGrid({1, 3, 0}, {8, 256}, {0, 23});
+    long long evaluations = 0;
+    const std::string whole = sameUnderEverySetting(
+        "arena wave", grid,
+        [&](const EngineRun& run, SliceStats& stats) {
+            return arenaMoves(playArenaGames(waveSlice(wave, 0, games), ac, run, &stats));
+        },
+        &evaluations);
     EngineRun run;
     run.backend = "hip";
-    const std::string joined = played(playArenaGames(waveSlice(wave, 0, 5), ac, run)) +
-                               played(playArenaGames(waveSlice(wave, 5, 9), ac, run));
-    expect(joined == whole, "slices [0, 5) and [5, 14) joined play the whole wave's games");
-    std::printf("arena: %d runs of a 14-game wave over 3 networks and a bot, %zu bytes of moves each\n", runs,
-                whole.size());
+    const std::string joined = arenaMoves(playArenaGames(waveSlice(wave, 0, cut), ac, run)) +
+                               arenaMoves(playArenaGames(waveSlice(wave, cut, games - cut), ac, run));
+    expect(joined == whole, "the wave's slices played apart join to the whole wave's games");
+    std::printf("arena: %zu settings of a %d-game wave over 3 networks and a bot, %zu bytes of moves each, "
+                "%lld positions evaluated\n",
+                grid.size(), games, whole.size(), evaluations);
 }
 
 } // namespace
 
 int main(int argc, char** argv) {
     if (argc != 2) {
-        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership|throughput|names|selfplay|arena\n");
+        std::printf("usage: hub_hip_driver chaos|failure|memory|refusals|drain|ownership|throughput|names|engines|selfplay|arena\n");
         return 2;
     }
     std::string why;
@@ -599,6 +735,7 @@ int main(int argc, char** argv) {
         else if (s == "drain") drain();
         else if (s == "throughput") throughput();
         else if (s == "names") names();
+        else if (s == "engines") engines();
         else if (s == "selfplay") selfplay();
         else if (s == "arena") arena();
         else {

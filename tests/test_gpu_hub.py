@@ -20,6 +20,12 @@ reference bench's hub load (256 threads of batch-8 requests, apps/bench.cpp:
 282-307), whose positions per second it prints. The name sites:
 checkBackendAvailable / cpuBackendName / makeBackend / the config's backend
 key and WorkerEvaluators(net, "hip", ...) (tests/test_cuda.cpp:1240-1258).
+The engine-spec sites: selfplay_engines / arena_engines naming hip engines
+round-trip (tests/test_config.cpp:764-780), the hosts file's hip_workers sets
+a hip engine's workers as cuda_workers does (tests/test_distributed.cpp:
+347-349, 411-421), the engine fingerprint ends with the GPU description, and
+the hub groups the coordinator's preflight checks are refused when they do
+not fit.
 Self-play slices on 5x5 and 9x9 networks and an arena wave of three networks
 and a bot, byte-identical across workers {1, 3, 8}, pass caps {8, 256} and
 chaos {off, on}, and the wave's slices joined equal to the whole
@@ -37,7 +43,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("scenario", ["chaos", "failure", "memory", "refusals", "drain", "ownership", "throughput",
-                                      "names", "selfplay", "arena"])
+                                      "names", "engines", "selfplay", "arena"])
 def test_reference_hub_drives_hip_runner(hip, scenario):
     # The driver is built beside the library (make -C oracle, from the
     # reference's sources): a library without it is an incomplete build, not
