@@ -41,7 +41,10 @@ def _hash(files):
     for f in files:
         with open(os.path.join(CSRC, f), "rb") as fh:
             h.update(fh.read())
-    h.update(" ".join(FLAGS).encode())
+    # The include directory by its place in the tree, not its absolute path:
+    # the header's text is hashed with the sources, so two checkouts of the
+    # same files hash alike wherever they are.
+    h.update(" ".join(FLAGS).replace(ROOT, "<repo>").encode())
     return h.hexdigest()[:8]
 
 
