@@ -76,6 +76,7 @@ def load():
             "azh_built": ([], C.c_int),
             "azh_available": ([C.c_char_p, C.c_size_t], C.c_int),
             "azh_describe": ([C.c_char_p, C.c_size_t], C.c_int),
+            "azh_device_cus": ([P(C.c_int)], C.c_int),
             "azh_last_error": ([], C.c_char_p),
             "azh_memory_need": ([P(NetCfg), C.c_int, C.c_int, P(C.c_size_t)], C.c_int),
             "azh_check_memory": ([P(NetCfg), C.c_int, C.c_int, C.c_int], C.c_int),
@@ -167,6 +168,13 @@ def describe():
     buf = C.create_string_buffer(512)
     _check(load().azh_describe(buf, 512))
     return buf.value.decode()
+
+
+def device_cus():
+    """The device's compute units, as the runner's launch rules count them."""
+    n = C.c_int()
+    _check(load().azh_device_cus(C.byref(n)))
+    return n.value
 
 
 def net_cfg(board, history, blocks, filters, value_hidden, ownership=0):

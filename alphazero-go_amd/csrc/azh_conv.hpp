@@ -87,6 +87,11 @@ __device__ __forceinline__ void loadEpilogue(EpilogueInputs<COW, PPW>& e, const 
                 const int p = min((pg0 + j) * 16 + n16, G::A - 1);
                 e.res[c][j] = skipq[(size_t)g * G::A + p];
             }
+    } else {
+#pragma unroll
+        for (int c = 0; c < COW; ++c)
+#pragma unroll
+            for (int j = 0; j < PPW; ++j) e.res[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 }
 
@@ -149,8 +154,9 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
 //    tiles);
 //  - a tap's A fragment is read from LDS one tap ahead, the B operands in
 //    the general body's ring;
-//  - the epilogue's BN factors and residual quads are read before the first
-//    MFMA (they do not depend on this convolution).
+//  - the epilogue's BN factors and, for a layer with a residual, its
+//    residual quads are read before the first MFMA (they do not depend on
+//    this convolution).
 // The MFMA sequence per output (chunk, tap, channel in chunk) and every
 // operand are the general body's, so the bits are too.
 template <int N, int WPG, int PPW, bool PLANAR>
@@ -282,10 +288,11 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
         }
     };
 
-    // The epilogue's inputs, unconditionally (without a residual, the
-    // output's own quads are read and ignored).
+    // The epilogue's inputs; residual quads only for a layer that adds one
+    // (a uniform branch: the count of loads in flight after it, which the
+    // chunks' waits use, is exact either way).
     EpilogueInputs<1, PPW> ep;
-    loadEpilogue<N, 1, PPW>(ep, scale, shift, skip ? skip : y, b, cout, cb0, pg0, k, n16);
+    loadEpilogue<N, 1, PPW>(ep, scale, shift, skip, b, cout, cb0, pg0, k, n16);
 
     f4 acc[1][PPW];
 #pragma unroll

@@ -1575,6 +1575,14 @@ int azh_describe(char* out, size_t cap) {
     });
 }
 
+int azh_device_cus(int* cus) {
+    return guarded([&] {
+        if (!cus) throw Error(AZH_ERR_ARGUMENT, "hip: bad arguments");
+        requireContext();
+        *cus = azh::deviceCUs();
+    });
+}
+
 const char* azh_last_error(void) { return gLastError.c_str(); }
 
 int azh_memory_need(const azh_netcfg* cfg, int max_batch, int slots, size_t* bytes) {

@@ -35,7 +35,7 @@ Beside the headline, "positions" times the steps either side of the pass
 (azh_evaluate_positions: encoding from stone bytes, the legal moves with
 superko, the priors) on the same boards, each position carrying 200
 superko hashes, with the oracle's CPU restatement of the same two steps
-timed on one host core.
+timed on the host's cores (one worker per CPU, as the pass's baseline).
 
 Runs on one GPU only: --gpus above 1 exits with a message.
 """
@@ -124,6 +124,16 @@ def host_cpus():
     return {"affinity": affinity, "cpu_count": os.cpu_count(), "cgroup_quota": quota}
 
 
+def cpu_workers():
+    """One CPU-baseline worker per CPU this process may run on (its affinity
+    set, within the container's CPU quota), and the host's counts."""
+    host = host_cpus()
+    workers = host["affinity"]
+    if host["cgroup_quota"]:
+        workers = max(1, min(workers, int(host["cgroup_quota"])))
+    return workers, host
+
+
 def cpu_baseline(workload, calls):
     """The oracle's blas pass (im2col + single-threaded OpenBLAS sgemm, the
     reference's CPU backend restated) on this host: one worker per CPU the
@@ -135,10 +145,7 @@ def cpu_baseline(workload, calls):
     import oracle as O
     w = O.WORKLOADS[workload]
     net = O.init_network(w.cfg)
-    host = host_cpus()
-    workers = host["affinity"]
-    if host["cgroup_quota"]:
-        workers = max(1, min(workers, int(host["cgroup_quota"])))
+    workers, host = cpu_workers()
     inp8, _ = O.workload_inputs(w, 8)
     rate, elapsed = O.time_workers(net, inp8, workers, calls, O.BLAS)
     one_b = min(w.batch, 256)
@@ -255,25 +262,16 @@ def positions_leg(r, w, B, seen_per_position, iters=20, passes=None):
 
 def positions_cpu_baseline(w, st, tm, seen, H, budget_s=3.0):
     """The oracle's encodePlanes + legal moves (Board::isLegal, hashAfter,
-    the superko scan) for the same positions on one host core."""
-    import numpy as np
+    the superko scan) for the same positions on the host: one
+    single-threaded worker per host CPU, as the pass's CPU baseline, each
+    taking the positions in turn for budget_s seconds."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    n = w.cfg[0]
-    t0 = time.perf_counter()
-    done = 0
-    while True:
-        for b in range(len(st)):
-            O.encode_planes(st[b:b + 1], n, int(tm[b]), H, b % 8)
-            O.legal_moves(st[b], n, int(tm[b]), seen[b])
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-        if time.perf_counter() - t0 > budget_s:
-            break
-    el = time.perf_counter() - t0
-    return {"value": round(done / el, 1), "unit": "positions/s", "cores": 1, "kind": "port",
-            "sample": f"{done} positions in {el:.1f} s (oracle encodePlanes + legal moves with superko)"}
+    workers, host = cpu_workers()
+    rate, el = O.time_positions_workers(st, tm, w.cfg[0], H, seen, workers, budget_s)
+    return {"value": round(rate, 1), "unit": "positions/s", "cores": workers, "host_cpus": host, "kind": "port",
+            "sample": f"{workers} single-threaded workers (one per host CPU), {round(rate * el)} positions in "
+                      f"{el:.1f} s (oracle encodePlanes + legal moves with superko)"}
 
 
 def main():

@@ -83,6 +83,14 @@ int azh_available(char* why, size_t cap);
  * runtime version and a hash of the kernel sources and flags. */
 int azh_describe(char* out, size_t cap);
 
+/* No counterpart in the reference: the compute units of the runner's device
+ * (the current one), as the launch rules count them: a pass alone runs its
+ * stem and tower as one board-resident launch when its batch gives one
+ * workgroup to 95% of them or fills whole rounds of them, and a pass splits
+ * into two half-batch chains by how its workgroups fill rounds of them.
+ * AZH_ERR_UNAVAILABLE without a usable GPU. */
+int azh_device_cus(int* cus);
+
 /* The message of the calling thread's last failed call ("" if none). */
 const char* azh_last_error(void);
 
@@ -196,7 +204,12 @@ int azh_infer(azh_runner* r, const float* input, int B, float* logits, float* va
  * array needs to start at zero (every element a pass reads is written
  * earlier in the same pass). The runner's device must be current; no slot
  * is used, so slots' passes may run meanwhile. Same kernels, same bits as
- * azh_infer. */
+ * azh_infer. The call takes the launch forms of a pass alone when no slot
+ * has a pass in flight; it is not itself counted as one (it may be captured
+ * into a graph and replayed, so the library cannot tell when it runs), so a
+ * slot's pass begun while it runs may take the forms of a pass alone too:
+ * the same bits, only the two passes' speed differs. Safe under stream
+ * capture (global mode): nothing on its path allocates or synchronizes. */
 int azh_infer_noalloc(azh_runner* r, const float* input, int B, float* logits, float* values, float* ownership,
                       void* stream);
 

@@ -1217,3 +1217,64 @@ double azo_time_workers(const azo_cfg* c, const float* params, const float* buff
     free(args);
     return dt > 0 ? (double)total / dt : 0.0;
 }
+
+/*
+ * The steps either side of the pass on the CPU, as the search does them per
+ * leaf (Mcts::evaluateLeaves encodes, src/mcts.cpp:113-134; Mcts::expand
+ * builds the legal set with superko, src/mcts.cpp:152-169): `workers`
+ * threads, each encoding and finding the legal moves of the B positions
+ * (stones [B][n*n], the current board only, H planes of history) in turn,
+ * over and over, until `budget` seconds have passed. Position b's superko
+ * list is seen[offsets[b] .. offsets[b+1]). Returns positions per second,
+ * all workers together; *elapsed the seconds.
+ */
+typedef struct {
+    const uint8_t *stones, *to_move;
+    const uint64_t* seen;
+    const int* offsets;
+    int n, H, B;
+    double stop;
+    long long positions;
+} positions_arg;
+
+static void* positions_main(void* p) {
+    positions_arg* w = p;
+    const int area = w->n * w->n;
+    float* planes = malloc(sizeof(float) * (size_t)(2 * w->H + 2) * area);
+    uint8_t* legal = malloc((size_t)area + 1);
+    w->positions = 0;
+    while (now_seconds() < w->stop) {
+        for (int b = 0; b < w->B; ++b) {
+            azo_encode_planes(w->stones + (size_t)b * area, 1, w->n, w->to_move[b], w->H, b % 8, planes);
+            azo_legal_moves(w->stones + (size_t)b * area, w->n, w->to_move[b], w->seen + w->offsets[b],
+                            w->offsets[b + 1] - w->offsets[b], legal);
+            ++w->positions;
+            if ((b & 15) == 15 && now_seconds() >= w->stop) break;
+        }
+    }
+    free(planes);
+    free(legal);
+    return NULL;
+}
+
+double azo_time_positions_workers(int n, int H, int B, const uint8_t* stones, const uint8_t* to_move,
+                                  const uint64_t* seen, const int* offsets, int workers, double budget,
+                                  double* elapsed) {
+    pthread_t* th = calloc((size_t)workers, sizeof(pthread_t));
+    positions_arg* args = calloc((size_t)workers, sizeof(positions_arg));
+    const double t0 = now_seconds();
+    for (int w = 0; w < workers; ++w) {
+        args[w] = (positions_arg){stones, to_move, seen, offsets, n, H, B, t0 + budget, 0};
+        pthread_create(&th[w], NULL, positions_main, &args[w]);
+    }
+    long long total = 0;
+    for (int w = 0; w < workers; ++w) {
+        pthread_join(th[w], NULL);
+        total += args[w].positions;
+    }
+    const double dt = now_seconds() - t0;
+    if (elapsed) *elapsed = dt;
+    free(th);
+    free(args);
+    return dt > 0 ? (double)total / dt : 0.0;
+}

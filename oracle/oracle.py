@@ -133,6 +133,9 @@ def _lib():
         h.azo_time_workers.argtypes = [P(Cfg), f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                        P(C.c_double)]
         h.azo_time_workers.restype = C.c_double
+        h.azo_time_positions_workers.argtypes = [C.c_int, C.c_int, C.c_int, u8, u8, u64p, P(C.c_int), C.c_int,
+                                                 C.c_double, P(C.c_double)]
+        h.azo_time_positions_workers.restype = C.c_double
         _lib.h = h
     return _lib.h
 
@@ -468,6 +471,23 @@ def time_workers(net: Net, inp, workers, calls, mode=BLAS, warm=True):
     el = C.c_double()
     rate = _lib().azo_time_workers(C.byref(net.cfg), fptr(net.params), fptr(net.buffers), fptr(inp), inp.shape[0],
                                    mode, workers, calls, int(warm), C.byref(el))
+    return rate, el.value
+
+
+def time_positions_workers(stones, to_move, n, H, seen, workers, budget):
+    """Positions/s of `workers` threads each encoding and finding the legal
+    moves (superko list seen[b] for position b) of the positions in turn for
+    `budget` seconds; returns (rate, elapsed seconds)."""
+    st = np.ascontiguousarray(stones, np.uint8).reshape(-1, n * n)
+    tm = np.ascontiguousarray(to_move, np.uint8)
+    lists = [np.asarray(x, np.uint64).reshape(-1) for x in seen]
+    offsets = np.zeros(len(lists) + 1, np.int32)
+    offsets[1:] = np.cumsum([x.size for x in lists])
+    flat = np.ascontiguousarray(np.concatenate(lists) if lists else np.zeros(0, np.uint64))
+    el = C.c_double()
+    rate = _lib().azo_time_positions_workers(n, H, st.shape[0], u8ptr(st), u8ptr(tm), _u64p(flat),
+                                             offsets.ctypes.data_as(C.POINTER(C.c_int)), workers, budget,
+                                             C.byref(el))
     return rate, el.value
 
 

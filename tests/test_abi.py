@@ -40,6 +40,11 @@ def test_built_and_describe_without_gpu_is_an_answer():
         with pytest.raises(azgo_hip.HipError) as e:
             azgo_hip.check_memory(to_hip_cfg(azgo_hip, O.WORKLOADS[1].cfg), 8, 1)
         assert e.value.code == azgo_hip.ERR_UNAVAILABLE
+        with pytest.raises(azgo_hip.HipError) as e:
+            azgo_hip.device_cus()
+        assert e.value.code == azgo_hip.ERR_UNAVAILABLE
+    else:
+        assert azgo_hip.device_cus() > 0
 
 
 def test_memory_need_formula():

@@ -320,28 +320,36 @@ def test_resident_tower_mode_refused(hip):
 
 
 def test_pass_forms(hip):
-    """How a pass runs, on the MI355X's 256 CUs: the board-resident tower for
-    a pass alone whose batch gives one workgroup to 95% of the CUs (or to
-    every CU in each of several rounds), the
-    half-batch chains beside another pass or on a part-filled round, the
-    small-board pass in one launch on 9x9 at 64 channels past 128 boards."""
+    """How a pass runs, from the device's compute units (C): the
+    board-resident tower for a pass alone whose batch gives one workgroup to
+    95% of the CUs (one round) or to every CU in each of several rounds;
+    otherwise, and beside another pass, the per-layer launches (on the
+    MI355X's 256 CUs in half-batch chains there); the small-board pass in one
+    launch on 9x9 at 64 channels past 128 boards."""
+    cus = hip.device_cus()
+    one_round = -(-19 * cus // 20)   # the fewest boards that give one workgroup to 95% of the CUs
     net = O.random_network(O.make_cfg(19, 2, 128), 613)
-    with _runner(hip, net, 512) as r:
-        assert r.pass_form(256) == r.FORM_RESIDENT
-        assert r.pass_form(244) == r.FORM_RESIDENT   # one round: from 95% of the CUs
-        assert r.pass_form(512) == r.FORM_RESIDENT
-        assert r.pass_form(256, alone=False) == r.FORM_SPLIT
-        assert r.pass_form(240) == r.FORM_SPLIT
-        assert r.pass_form(504) == r.FORM_SPLIT      # two rounds: only when full
+    with _runner(hip, net, 2 * cus) as r:
+        assert r.pass_form(cus) == r.FORM_RESIDENT
+        assert r.pass_form(one_round) == r.FORM_RESIDENT
+        assert not r.pass_form(one_round - 1) & r.FORM_RESIDENT
+        assert r.pass_form(2 * cus) == r.FORM_RESIDENT
+        assert not r.pass_form(2 * cus - 8) & r.FORM_RESIDENT   # two rounds: only when full
+        assert not r.pass_form(cus, alone=False) & r.FORM_RESIDENT
         assert r.pass_form(1) == 0
+        if cus == 256:
+            # The MI355X's measured forms beside them: two half-batch chains.
+            assert r.pass_form(256, alone=False) == r.FORM_SPLIT
+            assert r.pass_form(240) == r.FORM_SPLIT
+            assert r.pass_form(504) == r.FORM_SPLIT
         r.set_resident_tower(2)
-        assert r.pass_form(1) == r.FORM_RESIDENT and r.pass_form(256, alone=False) == r.FORM_RESIDENT
+        assert r.pass_form(1) == r.FORM_RESIDENT and r.pass_form(cus, alone=False) == r.FORM_RESIDENT
         r.set_resident_tower(0)
-        assert r.pass_form(256) == r.FORM_SPLIT
+        assert not r.pass_form(cus) & r.FORM_RESIDENT
         r.set_resident_tower(1)
-        r.input(0)[:256] = O.workload_inputs(O.Workload(0, "forms", net.cfg, 256, 0.3, 0.3), 256)[0]
-        r.stage(0, 256)
-        assert r.time_resident_tower(0, 256, 2) > 0 and r.time_resident_tower(0, 256, 2, stem=False) > 0
+        r.input(0)[:cus] = O.workload_inputs(O.Workload(0, "forms", net.cfg, cus, 0.3, 0.3), cus)[0]
+        r.stage(0, cus)
+        assert r.time_resident_tower(0, cus, 2) > 0 and r.time_resident_tower(0, cus, 2, stem=False) > 0
     net9 = O.random_network(O.make_cfg(9, 1, 64), 614)
     with _runner(hip, net9, 256) as r:
         assert r.pass_form(256) == r.FORM_SMALL
@@ -795,7 +803,7 @@ def test_mfma_probe(hip):
     MI355X), each wave 4 x chain MFMAs of 2048 flops, at a rate no higher
     than the published 157.3 TFLOP/s peak and not far below it."""
     ms, flops = hip.probe_mfma(2000, 2)
-    assert flops == 256 * 8 * 4 * 2000 * 2048
+    assert flops == hip.device_cus() * 8 * 4 * 2000 * 2048
     tf = flops / (ms / 2 * 1e-3) / 1e12
     assert 100.0 < tf <= 157.3 * 1.01, tf
     with pytest.raises(hip.HipError):

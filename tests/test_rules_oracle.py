@@ -168,3 +168,19 @@ def test_against_reference_on_random_boards():
                 rh = np.empty(n * n + 1, np.uint64)
                 h.ref_hash_after(O.u8ptr(s), n, tm, rh.ctypes.data_as(C.POINTER(C.c_uint64)))
                 assert np.array_equal(O.hash_after(s, n, tm), rh)
+
+
+def test_positions_workers_time_the_cpu_steps():
+    """The CPU baseline of the steps either side of the pass (bench.py's
+    positions leg): several threads encoding and finding legal moves with
+    superko lists run for the budget and count what they did."""
+    n = 9
+    boards = random_boards(n, 12, 7)
+    stones = np.stack(boards)
+    to_move = np.array([B_, W_] * 6, np.uint8)
+    g = np.random.default_rng(3)
+    seen = [g.integers(0, 2 ** 63, k, dtype=np.int64).astype(np.uint64) for k in range(12)]
+    one, el1 = O.time_positions_workers(stones, to_move, n, 8, seen, 1, 0.05)
+    two, el2 = O.time_positions_workers(stones, to_move, n, 8, seen, 2, 0.05)
+    assert el1 >= 0.05 and el2 >= 0.05
+    assert one > 0 and two > 0
