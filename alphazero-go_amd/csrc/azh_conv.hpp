@@ -136,7 +136,7 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
 //  - everything chunk q needs (its board planes, staged as the general body
 //    stages them, and its nine taps' A fragments for the block of 16
 //    channels, fetched once per workgroup instead of once per wave) is
-//    loaded into registers during chunk q - 2 and stored into LDS during
+//    loaded into registers during chunk q - 3 and stored into LDS during
 //    chunk q - 1, whose barrier publishes it;
 //  - the loads and stores are spread over the taps of the MFMA stream, one
 //    item per tap, on addresses computed once (a chunk adds only a uniform
@@ -146,9 +146,10 @@ __device__ __forceinline__ void storeOutputs(const f4 (&acc)[COW][PPW], const fl
 //    element and stores to a spare LDS cell; channels past cin are zeroed
 //    at the store): loads under a branch would leave the compiler's count
 //    of loads in flight unsure at the merge, and it would wait for all;
-//  - the load registers alternate between two sets with the chunks, and the
-//    chunk loop runs in pairs so that each set is fixed at compile time: no
-//    register copy waits on a load in flight;
+//  - the load registers alternate between two sets with the chunks (an
+//    item's store reads its set just before the item's next load fills it),
+//    and the chunk loop runs in pairs so that each set is fixed at compile
+//    time: no register copy waits on a load in flight;
 //  - the LDS tile holds only the board rows the workgroup's points touch,
 //    with a zero row above and below (the whole haloed board on the wider
 //    tiles);
@@ -298,30 +299,39 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
 #pragma unroll
     for (int j = 0; j < PPW; ++j) acc[0][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Chunks 0 and 1 in flight; chunk 0 published. A chunk past the last is
+    // Chunks 1 and 2 in flight in the two register sets; chunk 0 published
+    // (through a third set, live only here). A chunk past the last is
     // loaded as the last one again, stored into a buffer nobody reads
     // afterwards, and not multiplied.
     f4 p0[PER], a0[APER], p1[PER], a1[APER];
+    {
+        f4 pz[PER], az[APER];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) loadItem(i, 0, p0, a0);
+        for (int i = 0; i < NI; ++i) loadItem(i, 0, pz, az);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) loadItem(i, min(1, qLast), p1, a1);
-    __syncthreads();   // the zero fill is complete before any interior store
+        for (int i = 0; i < NI; ++i) loadItem(i, min(1, qLast), p0, a0);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) storeItem(i, 0, 0, p0, a0);
+        for (int i = 0; i < NI; ++i) loadItem(i, min(2, qLast), p1, a1);
+        __syncthreads();   // the zero fill is complete before any interior store
+#pragma unroll
+        for (int i = 0; i < NI; ++i) storeItem(i, 0, 0, pz, az);
+    }
     __syncthreads();
 
     constexpr int kRing = 4;
     constexpr int STEPS = 9 * PPW;
     auto tapOffset = [](int t) { return (t / 3) * G::H + (t % 3); };
-    // Chunk q from LDS buffer `buf` (q & 1): tap t loads items [t*NI/9,
-    // (t+1)*NI/9) of chunk q + 2 into the free register set (pNew, aNew) and
-    // stores the same items of chunk q + 1 (pNext, aNext: loaded during
-    // chunk q - 1) into the other buffer, free since the barrier that ended
-    // chunk q - 1. The last chunk stores a copy of itself there, never read.
-    auto chunk = [&](int q, int buf, f4 (&pNew)[PER], f4 (&aNew)[APER], const f4 (&pNext)[PER],
-                     const f4 (&aNext)[APER]) {
-        const int qn = min(q + 2, qLast), qs = min(q + 1, qLast);
+    // Chunk q from LDS buffer `buf` (q & 1): tap t stores items [t*NI/9,
+    // (t+1)*NI/9) of chunk q + 1 from the register set (ps, as), where they
+    // were loaded during chunk q - 2, into the other buffer (free since the
+    // barrier that ended chunk q - 1), and then loads the same items of
+    // chunk q + 3 into the registers the store has just read. A chunk's loads
+    // so have two chunks of MFMAs to arrive in (at small batches a chunk is
+    // shorter than a load's round trip), and the two register sets
+    // alternate with the chunks. The last chunks store copies of the last
+    // one there, never read.
+    auto chunk = [&](int q, int buf, f4 (&ps)[PER], f4 (&as)[APER]) {
+        const int qs = min(q + 1, qLast), ql = min(q + 3, qLast);
         const f4* bb = lds + buf * CB;
         const f4* ab = alds + buf * AITEMS + lane;
         f4 ring[kRing];
@@ -337,16 +347,16 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
                 const int i0 = t * NI / 9, i1 = (t + 1) * NI / 9;
 #pragma unroll
                 for (int it = i0; it < i1; ++it) {
-                    loadItem(it, qn, pNew, aNew);
+                    storeItem(it, buf ^ 1, qs, ps, as);
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                }
+#pragma unroll
+                for (int it = i0; it < i1; ++it) {
+                    loadItem(it, ql, ps, as);
                     if (it < PER)
                         __builtin_amdgcn_sched_group_barrier(0x020, PLANAR ? 4 : 1, 0);
                     else
                         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                }
-#pragma unroll
-                for (int it = i0; it < i1; ++it) {
-                    storeItem(it, buf ^ 1, qs, pNext, aNext);
-                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
                 }
                 if (t + 1 < 9) {
                     aT[(t + 1) & 1] = ab[(t + 1) * 64];   // the next tap's fragment, a tap ahead
@@ -369,10 +379,10 @@ __device__ __forceinline__ void conv3x3SmallBody(const float* __restrict__ x, co
     const int nqQuads = tail ? nq - 1 : nq;
     int q = 0;
     for (; q + 1 < nqQuads; q += 2) {
-        chunk(q, 0, p0, a0, p1, a1);
-        chunk(q + 1, 1, p1, a1, p0, a0);
+        chunk(q, 0, p0, a0);
+        chunk(q + 1, 1, p1, a1);
     }
-    if (q < nqQuads) chunk(q, 0, p0, a0, p1, a1);
+    if (q < nqQuads) chunk(q, 0, p0, a0);
     if (tail) {
         const int ql = nq - 1, buf = ql & 1;
         // rofs[j] - k * GC is the lane's top-left cell.

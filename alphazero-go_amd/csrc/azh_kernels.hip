@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 
@@ -42,9 +43,10 @@ hipError_t launchConvN(const float* x, const float* wp, const float* scale, cons
 // ------------------------------------------------------------------ heads
 
 // The heads' 1x1 convolutions F -> 2 (policy) and F -> 1 (value), their BN
-// and ReLU (src/network.cpp:274-277, 288-291), one position per workgroup and
-// one point per thread, the trunk read in channel quads (32 16-byte loads
-// per 128 channels) ahead of their FMAs:
+// and ReLU (src/network.cpp:274-277, 288-291), one point per thread and a
+// position's points over gridDim.y workgroups (blockIdx.x the position), the
+// trunk read in channel quads (32 16-byte loads per 128 channels) ahead of
+// their FMAs:
 // act [B][3][A], planes 0-1 the policy's flattened [2A] row (feature c*A + p,
 // src/network.cpp:278-285), plane 2 the value's [A] row. With own set, the
 // ownership head too: 1x1 conv F -> 1, BN, tanh at every point, no ReLU
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(((N * N + 63) / 64) * 64) void headConvKernel(const
     // (they start at +0 and never become -0), so the straight-line loop
     // rounds exactly as the sum over channels 0..F-1 does.
     __shared__ f4 wsh[kRound];
-    const int b = blockIdx.x, p = threadIdx.x;
+    const int b = blockIdx.x, p = blockIdx.y * blockDim.x + threadIdx.x;
     const bool withOwn = own != nullptr;
     const int quads = (F + 3) / 4;
     const f4* tq = reinterpret_cast<const f4*>(trunk) + (size_t)b * quads * A + min(p, A - 1);
@@ -419,9 +421,14 @@ hipError_t launchHeads(const float* trunk, const HeadWeights& w, float* act, flo
                        float* own, int B, int n, int F, int V, hipStream_t stream) {
     if (B < 1) return hipSuccess;
     if (V > 256) return hipErrorInvalidValue;
-    const int A1 = n * n + 1;
-    const dim3 grid1(B), grid2(ceilDiv(B, kFcBoards), ceilDiv(A1, kFcOutTile) + 1);
-    const dim3 block1(ceilDiv(n * n, 64) * 64), block2(256);
+    const int A = n * n, A1 = A + 1;
+    // A small batch spreads each position's points over up to three
+    // workgroups, so more CUs read the trunk (19x19 at batch 1: three of 128
+    // threads instead of one of 384); the same per-point arithmetic either way.
+    const int slices = std::max(1, std::min(3, (int)(deviceCUs() / (2L * B))));
+    const int threads = ceilDiv(ceilDiv(A, slices), 64) * 64;
+    const dim3 grid1(B, ceilDiv(A, threads)), grid2(ceilDiv(B, kFcBoards), ceilDiv(A1, kFcOutTile) + 1);
+    const dim3 block1(threads), block2(256);
     switch (n) {
 #define AZH_HEADS(NN)                                                                                         \
     case NN:                                                                                                  \

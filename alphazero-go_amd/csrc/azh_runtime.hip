@@ -1427,6 +1427,7 @@ void createRunner(const azh_netcfg* cfg, const azh_tensor* tensors, int count, i
     std::unique_ptr<azh_runner> r(new azh_runner(*cfg, max_batch));
     check(hipGetDevice(&r->device), "hipGetDevice");
     scratchOnCurrentDevice();   // azh_infer_noalloc's scratch, resolved at set-up on the runner's device
+    azh::deviceCUs();           // the launch rules' CU count, read once here, not during a caller's capture
     uploadWeights(*cfg, given, r->weights);
     r->initTowerLayout();
     for (int i = 0; i < slots; ++i) r->slots.push_back(std::make_unique<Slot>(r->shape, max_batch));

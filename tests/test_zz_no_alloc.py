@@ -4,8 +4,11 @@ a caller's stream. Checked against azh_infer, the entry point it varies, on
 the same positions: the same kernels, so the same bits, for logits, values
 and ownership; two calls in a row on the same stream, the second with a
 smaller batch (the scratch keeps the first call's contents); the
-small-board one-launch pass and the per-layer launches; and a batch above
-the scratch array's capacity refused before anything runs.
+small-board one-launch pass and the per-layer launches; the call captured
+into a HIP graph on the caller's stream (global capture mode, so any
+allocation or synchronizing call on its path would fail the capture) and the
+graph launched twice, each launch equal to azh_infer; and a batch above the
+scratch array's capacity refused before anything runs.
 
 The test allocates its device arrays and stream through the HIP runtime
 (the entry point never does).
@@ -34,6 +37,13 @@ class Hip:
         self.lib.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
         self.lib.hipStreamSynchronize.argtypes = [C.c_void_p]
         self.lib.hipStreamDestroy.argtypes = [C.c_void_p]
+        self.lib.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.lib.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.lib.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p,
+                                                 C.c_size_t]
+        self.lib.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.lib.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.lib.hipGraphDestroy.argtypes = [C.c_void_p]
         self.held = []
 
     def ok(self, rc, what):
@@ -145,3 +155,53 @@ def test_noalloc_refuses_beyond_scratch(hip):
             assert bitwise_equal(rt.download(d_v, (1,)), want[1])
     finally:
         rt.close()
+
+
+# Captured with hipStreamCaptureModeGlobal: a call on the entry point's path
+# that allocates or synchronizes would end the capture with an error.
+CAPTURE_GLOBAL = 0
+
+
+@pytest.mark.parametrize("name,make,w,B1,B2,own", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_under_graph_capture(hip, name, make, w, B1, B2, own):
+    """azh_infer_noalloc as a caller under HIP graph capture uses it: begin
+    capture on the caller's stream, the call, end capture, instantiate, then
+    two launches of the graph, each output equal to azh_infer's bits. The
+    input changes between the launches (the second batch's positions copied
+    over the first's), so the second launch cannot pass on stale outputs."""
+    net = make()
+    cfg = net.cfg
+    inp, _ = O.workload_inputs(O.Workload(w.tag, w.name, cfg, B1, w.p_black, w.p_white), B1)
+    other, _ = O.workload_inputs(O.Workload(w.tag + 1, w.name, cfg, B1, w.p_black, w.p_white), B1)
+    print(f"{name}: azh_infer_noalloc captured at B={B1}", flush=True)
+    rt = Hip()
+    stream = rt.stream()
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        with hip.Runner(to_hip_cfg(hip, cfg), net.tensors(), B1, 1) as r:
+            wants = [r.infer(x, ownership=own) for x in (inp, other)]
+            d_in = rt.upload(inp.astype(np.float32))
+            d_l, d_v = rt.filled((B1, cfg.actions)), rt.filled((B1,))
+            d_o = rt.filled((B1, cfg.area)) if own else None
+            rt.ok(rt.lib.hipStreamBeginCapture(stream, CAPTURE_GLOBAL), "hipStreamBeginCapture")
+            try:
+                r.infer_noalloc(d_in, B1, d_l, d_v, d_o, stream)
+            finally:
+                rt.ok(rt.lib.hipStreamEndCapture(stream, C.byref(graph)), "hipStreamEndCapture")
+            rt.ok(rt.lib.hipGraphInstantiate(C.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+            for x, want in zip((inp, other), wants):
+                a = np.ascontiguousarray(x, np.float32)
+                rt.ok(rt.lib.hipMemcpy(d_in, a.ctypes.data, a.nbytes, H2D), "hipMemcpy")
+                rt.ok(rt.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+                rt.ok(rt.lib.hipStreamSynchronize(stream), "hipStreamSynchronize")
+                got = [rt.download(d_l, (B1, cfg.actions)), rt.download(d_v, (B1,))]
+                if own:
+                    got.append(rt.download(d_o, (B1, cfg.area)))
+                for g, e in zip(got, want):
+                    assert bitwise_equal(g, e), name
+    finally:
+        if exe.value:
+            rt.lib.hipGraphExecDestroy(exe)
+        if graph.value:
+            rt.lib.hipGraphDestroy(graph)
+        rt.close(stream)
