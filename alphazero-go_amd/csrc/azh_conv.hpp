@@ -87,12 +87,9 @@ __device__ __forceinline__ void loadEpilogue(EpilogueInputs<COW, PPW>& e, const 
                 const int p = min((pg0 + j) * 16 + n16, G::A - 1);
                 e.res[c][j] = skipq[(size_t)g * G::A + p];
             }
-    } else {
-#pragma unroll
-        for (int c = 0; c < COW; ++c)
-#pragma unroll
-            for (int j = 0; j < PPW; ++j) e.res[c][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    // Without a residual e.res stays unset: writeOutputs then adds nothing
+    // and never uses it.
 }
 
 template <int N, int COW, int PPW>

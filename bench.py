@@ -180,7 +180,8 @@ def copy_calibration(mib, iters):
 def mfma_calibration(iters):
     """The fp32 matrix units' rate with nothing else in the way: one 8-wave
     workgroup per CU, each wave a dependent chain of 80,000 16x16x4 MFMAs
-    (one per 32 cycles per SIMD): the clock the chip holds under a full
+    (two waves per SIMD, so each SIMD alternates between two chains and
+    issues one MFMA every 32 cycles): the clock the chip holds under a full
     MFMA load, against the 2.4 GHz of the published peak."""
     import azgo_hip
     ms, flops = azgo_hip.probe_mfma(20000, iters)
