@@ -218,10 +218,11 @@ __global__ void fillKernel(float* data, size_t n, float value) {
 
 // The matrix units' rate with nothing else in the way: 8 waves per
 // workgroup (two per SIMD), each a dependent chain of 4 * chain
-// v_mfma_f32_16x16x4_f32 on one accumulator (a dependent chain issues one
-// MFMA per 32 cycles, as independent ones do). The operands are tiny, so
-// the sums stay finite; one float per thread is written so the chain is
-// kept.
+// v_mfma_f32_16x16x4_f32 on one accumulator. The SIMD alternates between
+// its two waves' chains and so issues one MFMA every 32 cycles (a single
+// dependent chain alone on a SIMD issues one only every 44). The operands
+// are tiny, so the sums stay finite; one float per thread is written so the
+// chain is kept.
 __global__ __launch_bounds__(512) void mfmaChainKernel(float* out, int chain) {
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const float a = 1.0f + threadIdx.x * 1e-7f, b = 1e-9f;
