@@ -25,10 +25,8 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-4   # max-abs on logits and values (the parity bar)
 
 # (calibration tag, network config, GPU batch, positions checked on the CPU).
-# The 20x256 net's pass runs at its benchmark batch of 512; the CPU checks a
-# spread of 64 of its positions on a pool of threads (each position's
-# outputs depend on its own input only: batch independence, tested bitwise
-# elsewhere).
+# Every position of every batch is checked; the 20x256 net's 512 on a pool
+# of threads (each position's outputs depend on its own input only).
 CASES = [
     ("1", O.WORKLOADS[1].cfg, 8, 8),
     ("2", O.WORKLOADS[2].cfg, 64, 64),
@@ -37,7 +35,7 @@ CASES = [
     ("3", O.WORKLOADS[3].cfg, 8, 8),
     ("3", O.WORKLOADS[3].cfg, 32, 32),
     ("3v256", O.make_cfg(19, 10, 128, value_hidden=256), 64, 64),
-    ("5", O.WORKLOADS[5].cfg, 512, 64),
+    ("5", O.WORKLOADS[5].cfg, 512, 512),
 ]
 
 
